@@ -1,0 +1,142 @@
+/*
+ * vcpp_attention.h -- C ABI of the MI355X paged-attention library
+ * (libvcpp_attn.so, built from vllm-cpp_amd/csrc for gfx950).
+ *
+ * Two layers:
+ *   v1  the reference launcher signatures of cuda/attention.h:19-45, with
+ *       C linkage, so code written against that header links unchanged;
+ *   v2  descriptor entry points that carry what v1 leaves implicit (separate
+ *       K/V bases, strides, KV dtype, device-side lengths, stream, workspace)
+ *       and return a status code.  v1 is a thin wrapper over v2.
+ *
+ * Conventions shared by every entry point:
+ *   - all tensor pointers are caller-owned device memory unless stated;
+ *   - `half` data is IEEE binary16 passed as uint16_t (ABI-equal to half);
+ *   - streams are hipStream_t passed as void* (NULL = the null stream);
+ *   - calls are asynchronous on their stream; calls that share a stream are
+ *     ordered, calls on different streams that share a workspace race;
+ *   - v2 entry points return VCPP_OK (0) or a negative VCPP_E* code and record
+ *     a message retrievable with vcpp_last_error() (thread-local).  Nothing
+ *     ever calls exit().
+ *
+ * Attention semantics (reference src/paged_attention.cpp:11-90): for query
+ * head h the KV head is h / (num_heads / num_kv_heads); logits are
+ * q.k / sqrt(head_dim); out = sum_p exp(s_p - max) v_p / (sum_p exp(s_p - max)
+ * + 1e-9).  Positions p < context_len whose logical block p / block_size is at
+ * or past the table length, or whose physical block id is outside
+ * [0, num_blocks), are skipped.  A sequence with no usable position gets zeros.
+ */
+#ifndef VCPP_ATTENTION_H
+#define VCPP_ATTENTION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define VCPP_OK 0
+#define VCPP_E_INVALID (-1)     /* bad argument (shape, dtype, null pointer) */
+#define VCPP_E_UNSUPPORTED (-2) /* valid but not implemented for this shape */
+#define VCPP_E_WORKSPACE (-3)   /* workspace missing or too small */
+#define VCPP_E_HIP (-4)         /* HIP runtime error (message has details) */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* vcpp_last_error(void);
+/* Library version string. */
+const char* vcpp_version(void);
+
+/* ---- KV page description ----------------------------------------------- */
+#define VCPP_KV_F32 0
+#define VCPP_KV_F16 1
+#define VCPP_KV_I8 2 /* symmetric int8, one fp16 scale per (token, kv head) */
+
+/*
+ * One layer of a paged KV pool.  Block b's K page is
+ *   k + b * block_stride   (elements of the KV dtype),
+ * laid out [block_size tokens][num_kv_heads][head_dim] -- the per-(block,
+ * layer) slab of the reference BlockPool (src/kv_cache_manager.cpp:12-34,
+ * 90-95).  V likewise.  With the reference's "all layers in one block"
+ * allocation, pass k = base + layer * block_size * kv_dim and
+ * block_stride = num_layers * block_size * kv_dim.
+ * VCPP_KV_I8 adds fp16 scale pages: block b's K scales are
+ *   k_scale + b * scale_block_stride,  laid out [num_kv_heads][block_size].
+ * Requirements: head_dim % 16 == 0, block_size % 16 == 0, 16-byte aligned
+ * bases and row starts (block_stride * elem_size and head_dim * elem_size
+ * multiples of 16 for F16/F32, of 8 for I8).
+ */
+typedef struct vcpp_kv_pages {
+    int32_t dtype;
+    int32_t block_size;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int64_t num_blocks;
+    int64_t block_stride;
+    int64_t scale_block_stride;
+    const void* k;
+    const void* v;
+    const uint16_t* k_scale;
+    const uint16_t* v_scale;
+} vcpp_kv_pages;
+
+/* ---- v2: batched paged decode ------------------------------------------ */
+
+/*
+ * Batched decode attention, one query token per sequence.
+ *   q            [num_seqs][num_heads][head_dim] fp32
+ *   out          [num_seqs][num_heads][head_dim] fp32 (overwritten)
+ *   block_tables [num_seqs][max_blocks_per_seq] int32 physical block ids
+ *   table_lens   [num_seqs] int32 usable entries per row, or NULL (= all
+ *                max_blocks_per_seq) -- the reference's block_table.size()
+ *   context_lens [num_seqs] int32 on the device
+ *   max_context_len  host-side upper bound of context_lens (sizes the grid;
+ *                a larger context_len is an error the kernel cannot report:
+ *                positions past max_context_len are not attended)
+ *   partition_size   tokens per split-K partition (multiple of 32, <= 1024;
+ *                0 = library default).  Sequences longer than one partition
+ *                are reduced by a log-sum-exp merge kernel.
+ *   workspace    device scratch of at least vcpp_decode_workspace_size(...)
+ *                bytes (may be NULL when that size is 0).
+ * Replaces the per-request loop around paged_attention()
+ * (src/paged_engine.cpp:505-508, src/paged_attention.cpp:96-121).
+ */
+int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
+                      const int32_t* block_tables, int32_t max_blocks_per_seq,
+                      const int32_t* table_lens, const int32_t* context_lens,
+                      int32_t num_seqs, int32_t max_context_len, int32_t num_heads,
+                      int32_t partition_size, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+size_t vcpp_decode_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t head_dim,
+                                  int32_t max_context_len, int32_t partition_size);
+
+/* Partition size the library uses when partition_size == 0. */
+int32_t vcpp_decode_default_partition(int32_t num_seqs, int32_t num_kv_heads,
+                                      int32_t max_context_len);
+
+/* ---- v1: reference launcher signatures (cuda/attention.h) -------------- */
+
+/*
+ * cuda/attention.h:19-30.  Defined here (the reference leaves these open):
+ *   q, out        [batch_size][num_heads][head_dim] fp32
+ *   kv_cache      fp16 pages [num_blocks][2 (K, V)][block_size][num_kv_heads][head_dim]
+ *                 (K and V behind the one pointer; num_blocks is not passed,
+ *                 so block ids are trusted)
+ *   block_tables  [batch_size][max_b ceil(context_lens[b] / block_size)] int32
+ *   context_lens  HOST int32 [batch_size] (the reference reads it on the host,
+ *                 cuda/attention.cu:25-28); the library stages a device copy.
+ *   block_size    16 or 32; anything else launches nothing and records
+ *                 VCPP_E_UNSUPPORTED in vcpp_last_error().
+ * Runs on the null stream, asynchronously; uses a library-owned workspace.
+ */
+void paged_attention_cuda(const float* q, const uint16_t* kv_cache, const int32_t* block_tables,
+                          const int32_t* context_lens, float* out, int32_t num_heads,
+                          int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                          int32_t batch_size);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,154 @@
+"""GPU parity of the paged decode path (vcpp_paged_decode / paged_attention_cuda)
+against the CPU oracle on identical seeded inputs.
+
+Tolerances (numpy allclose form, err <= atol + rtol * |want|):
+  fp32 KV: atol 1e-4, rtol 1e-4;  fp16 / int8 KV: atol 2e-3, rtol 1e-2.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+import pyvcpp
+from gpu_util import DevPool, assert_close, dev, gpu_decode
+
+pytestmark = pytest.mark.gpu
+
+TOL = {O.ORC_F32: (1e-4, 1e-4), O.ORC_F16: (2e-3, 1e-2), O.ORC_I8: (2e-3, 1e-2)}
+
+
+def random_tables(seed, ctx, num_blocks, max_blocks=None):
+    nbs = [(c + O.BS - 1) // O.BS for c in ctx]
+    mb = max(max(nbs), 1) if max_blocks is None else max_blocks
+    perm = O.permutation(seed, num_blocks)
+    t = np.full((len(ctx), mb), -1, dtype=np.int32)
+    k = 0
+    for i, n in enumerate(nbs):
+        t[i, :n] = perm[k:k + n]
+        k += n
+    assert k <= num_blocks
+    return t
+
+
+def config1(kind=O.ORC_F32):
+    """1 seq, ctx 512, 64/8 heads, D 80, 32 logical blocks on
+    a random permutation of 64 physical blocks, N(0,1)."""
+    pool = O.make_pool(kind, 101, 64, 8, 80)
+    q = O.normal(103, (1, 64, 80))
+    table = O.permutation(107, 64)[:32].reshape(1, 32)
+    return pool, q, table, np.array([512], dtype=np.int32)
+
+
+@pytest.mark.parametrize("kind", [O.ORC_F32, O.ORC_F16, O.ORC_I8])
+@pytest.mark.parametrize("partition", [0, 64, 512])
+def test_config1(cuda, kind, partition):
+    pool, q, table, ctx = config1(kind)
+    want = O.decode(pool, q, table, ctx, 64)
+    got = gpu_decode(DevPool(pool), q, table, ctx, 64, partition_size=partition)
+    assert_close(got, want, *TOL[kind], what="config1 kind=%d P=%d" % (kind, partition))
+
+
+@pytest.mark.parametrize("kind", [O.ORC_F32, O.ORC_F16, O.ORC_I8])
+@pytest.mark.parametrize("heads", [(1, 1), (8, 1), (64, 8), (12, 4), (32, 2)])
+def test_small_cases(cuda, kind, heads):
+    H, Hkv = heads
+    ctx = np.array([0, 1, 15, 16, 17, 33, 100, 257], dtype=np.int32)
+    nb = 64
+    pool = O.make_pool(kind, 11 + H, nb, Hkv, 80)
+    q = O.normal(13 + H, (len(ctx), H, 80))
+    tables = random_tables(17, ctx, nb)
+    want = O.decode(pool, q, tables, ctx, H)
+    got = gpu_decode(DevPool(pool), q, tables, ctx, H, partition_size=64)
+    assert_close(got, want, *TOL[kind], what="small H=%d Hkv=%d kind=%d" % (H, Hkv, kind))
+    assert np.all(got[0] == 0.0), "ctx=0 must give zeros"
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_other_head_dims(cuda, D):
+    ctx = np.array([5, 48, 300], dtype=np.int32)
+    pool = O.make_pool(O.ORC_F16, 21, 40, 8, D)
+    q = O.normal(23, (3, 64, D))
+    tables = random_tables(29, ctx, 40)
+    want = O.decode(pool, q, tables, ctx, 64)
+    got = gpu_decode(DevPool(pool), q, tables, ctx, 64, partition_size=128)
+    assert_close(got, want, *TOL[O.ORC_F16], what="D=%d" % D)
+
+
+@pytest.mark.parametrize("kind", [O.ORC_F32, O.ORC_F16, O.ORC_I8])
+def test_skip_rules(cuda, kind):
+    """Invalid block ids and positions past the table are skipped, as the
+    reference does (src/paged_attention.cpp:38,42)."""
+    nb = 48
+    pool = O.make_pool(kind, 31, nb, 8, 80)
+    ctx = np.array([200, 200, 200, 64], dtype=np.int32)
+    q = O.normal(37, (4, 64, 80))
+    tables = random_tables(41, ctx, nb)
+    tables[0, 3] = -5          # negative id
+    tables[1, 7] = nb + 100    # id past the pool
+    table_lens = np.array([13, 13, 6, 2], dtype=np.int32)  # row 2/3 shorter than ctx
+    want = O.decode(pool, q, tables, ctx, 64, table_lens=table_lens)
+    got = gpu_decode(DevPool(pool), q, tables, ctx, 64, table_lens=table_lens,
+                     partition_size=64)
+    assert_close(got, want, *TOL[kind], what="skip rules kind=%d" % kind)
+
+
+def test_all_positions_skipped_gives_zero(cuda):
+    pool = O.make_pool(O.ORC_F16, 43, 8, 8, 80)
+    ctx = np.array([40, 40], dtype=np.int32)
+    q = O.normal(47, (2, 64, 80))
+    tables = np.full((2, 3), -1, dtype=np.int32)
+    got = gpu_decode(DevPool(pool), q, tables, ctx, 64, partition_size=32)
+    assert np.all(got == 0.0)
+
+
+def test_split_invariance(cuda):
+    """The same sequences with every partition size agree with the oracle."""
+    nb = 600
+    pool = O.make_pool(O.ORC_F16, 53, nb, 8, 80)
+    ctx = np.array([4000, 1, 777, 2048, 33], dtype=np.int32)
+    q = O.normal(59, (5, 64, 80))
+    tables = random_tables(61, ctx, nb)
+    want = O.decode(pool, q, tables, ctx, 64)
+    dp = DevPool(pool)
+    outs = []
+    for P in (32, 96, 256, 1024):
+        got = gpu_decode(dp, q, tables, ctx, 64, partition_size=P)
+        assert_close(got, want, *TOL[O.ORC_F16], what="P=%d" % P)
+        outs.append(got)
+    for o in outs[1:]:
+        assert np.max(np.abs(o - outs[0])) < 1e-4
+
+
+def test_config2_full(cuda):
+    """BASELINE config 2 at full size: 64 seqs, ctx U[128,4096], fp16 pages in a
+    pool of 1.25x the tokens, random tables; every output checked."""
+    ctx = O.uniform_int(71, 64, 128, 4096)
+    nb = int(np.ceil(1.25 * ctx.sum() / O.BS))
+    pool = O.make_pool(O.ORC_F16, 73, nb, 8, 80)
+    q = O.normal(79, (64, 64, 80))
+    tables = random_tables(83, ctx, nb)
+    want = O.decode(pool, q, tables, ctx, 64)
+    got = gpu_decode(DevPool(pool), q, tables, ctx, 64)
+    assert_close(got, want, *TOL[O.ORC_F16], what="config2")
+
+
+def test_v1_entry(cuda):
+    """paged_attention_cuda (cuda/attention.h:19-30) on the v1 layout
+    [nb][2][BS][Hkv][D] with host context_lens."""
+    nb = 80
+    pool = O.make_pool(O.ORC_F16, 89, nb, 8, 80)
+    ctx = np.array([300, 5, 129], dtype=np.int32)
+    q = O.normal(97, (3, 64, 80))
+    tables = random_tables(101, ctx, nb)
+    want = O.decode(pool, q, tables, ctx, 64)
+    kv = np.stack([pool.k, pool.v], axis=1)  # [nb][2][BS][Hkv][D]
+    kvd = dev(kv)
+    qd = dev(q)
+    out = torch.zeros_like(qd)
+    td = dev(tables)
+    L = pyvcpp.lib()
+    L.paged_attention_cuda(qd.data_ptr(), kvd.data_ptr(), td.data_ptr(), ctx.ctypes.data,
+                           out.data_ptr(), 64, 8, 80, 16, 3)
+    torch.cuda.synchronize()
+    assert pyvcpp.last_error() == ""
+    assert_close(out.cpu().numpy(), want, *TOL[O.ORC_F16], what="v1")

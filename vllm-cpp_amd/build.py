@@ -1,0 +1,57 @@
+"""Builds libvcpp_attn.so (the gfx950 paged-attention library) in-tree.
+
+Usage: python vllm-cpp_amd/build.py   (or __graft_entry__.build()).
+Every HIP source is compiled for gfx950 only, with packed-fp32 instruction
+selection disabled, and linked into one shared library next to this file.
+"""
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIB = os.path.join(HERE, "libvcpp_attn.so")
+SOURCES = ["csrc/decode.hip", "csrc/api.cpp"]
+HEADERS = ["csrc/decode.h", "csrc/device_common.h"]
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", os.path.join(ROOT, "include"),
+    "-I", os.path.join(HERE, "csrc"),
+]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature.
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in r.stderr.splitlines() if noise not in l)
+    if r.returncode != 0:
+        raise RuntimeError("build failed: %s\n%s" % (" ".join(cmd), err))
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+
+
+def build(verbose=False):
+    objs = []
+    os.makedirs(os.path.join(HERE, "_build"), exist_ok=True)
+    for src in SOURCES:
+        obj = os.path.join(HERE, "_build", os.path.basename(src) + ".o")
+        lang = ["-x", "hip"]
+        _run([HIPCC] + FLAGS + lang + ["-c", os.path.join(HERE, src), "-o", obj], verbose)
+        objs.append(obj)
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", LIB] + objs, verbose)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,263 @@
+// api.cpp -- extern "C" entry points of libvcpp_attn.so (include/vcpp_attention.h).
+//
+// Argument checking, workspace sizing and the v1 shims live here; the kernels
+// live in decode.hip / prefill.hip.  Errors never terminate the process: v2
+// returns a VCPP_E* code, v1 (void, like cuda/attention.h) records it, and
+// both leave the message in a thread-local string for vcpp_last_error().
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "decode.h"
+#include "vcpp_attention.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(VCPP_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr int32_t kDefaultPartition = 256;
+constexpr int32_t kMaxPartition = 1024;
+
+int32_t ceil_div(int64_t a, int64_t b) { return (int32_t)((a + b - 1) / b); }
+
+int32_t resolve_partition(int32_t partition_size) {
+    return partition_size > 0 ? partition_size : kDefaultPartition;
+}
+
+int32_t num_parts(int32_t max_context_len, int32_t partition) {
+    return max_context_len <= 0 ? 1 : ceil_div(max_context_len, partition);
+}
+
+size_t decode_ws_bytes(int32_t num_seqs, int32_t num_heads, int32_t head_dim, int32_t parts) {
+    if (parts <= 1) return 0;
+    const size_t rows = (size_t)num_seqs * parts * num_heads;
+    // o partials, then (m, l) pairs; both 256-byte aligned.
+    const size_t o_bytes = ((rows * head_dim * sizeof(float)) + 255) & ~size_t(255);
+    return o_bytes + ((rows * sizeof(float2) + 255) & ~size_t(255));
+}
+
+int check_pages(const vcpp_kv_pages* kv) {
+    if (!kv) return fail(VCPP_E_INVALID, "kv pages descriptor is NULL");
+    if (kv->dtype != VCPP_KV_F32 && kv->dtype != VCPP_KV_F16 && kv->dtype != VCPP_KV_I8)
+        return fail(VCPP_E_INVALID, "unknown kv dtype %d", kv->dtype);
+    if (kv->block_size <= 0 || kv->block_size % 16 != 0)
+        return fail(VCPP_E_UNSUPPORTED, "block_size %d is not a positive multiple of 16",
+                    kv->block_size);
+    if (kv->num_kv_heads <= 0) return fail(VCPP_E_INVALID, "num_kv_heads must be positive");
+    if (kv->num_blocks < 0) return fail(VCPP_E_INVALID, "num_blocks must be >= 0");
+    if (!vcpp::decode_head_dim_supported(kv->dtype, kv->head_dim))
+        return fail(VCPP_E_UNSUPPORTED, "head_dim %d not supported for kv dtype %d",
+                    kv->head_dim, kv->dtype);
+    if (kv->num_blocks > 0 && (!kv->k || !kv->v))
+        return fail(VCPP_E_INVALID, "K/V page base is NULL");
+    const int64_t esize = kv->dtype == VCPP_KV_F32 ? 4 : kv->dtype == VCPP_KV_F16 ? 2 : 1;
+    const int64_t align = kv->dtype == VCPP_KV_I8 ? 8 : 16;
+    if ((kv->block_stride * esize) % align != 0 || (kv->head_dim * esize) % align != 0 ||
+        (reinterpret_cast<uintptr_t>(kv->k) % align) != 0 ||
+        (reinterpret_cast<uintptr_t>(kv->v) % align) != 0)
+        return fail(VCPP_E_INVALID, "K/V pages must be %lld-byte aligned (bases and strides)",
+                    (long long)align);
+    if (kv->block_stride < (int64_t)kv->block_size * kv->num_kv_heads * kv->head_dim)
+        return fail(VCPP_E_INVALID, "block_stride %lld smaller than one page",
+                    (long long)kv->block_stride);
+    if (kv->dtype == VCPP_KV_I8) {
+        if (kv->num_blocks > 0 && (!kv->k_scale || !kv->v_scale))
+            return fail(VCPP_E_INVALID, "int8 pages need k_scale and v_scale");
+        if (kv->scale_block_stride < (int64_t)kv->num_kv_heads * kv->block_size ||
+            kv->scale_block_stride % 4 != 0 ||
+            reinterpret_cast<uintptr_t>(kv->k_scale) % 8 != 0 ||
+            reinterpret_cast<uintptr_t>(kv->v_scale) % 8 != 0)
+            return fail(VCPP_E_INVALID,
+                        "scale pages must be 8-byte aligned with scale_block_stride a multiple "
+                        "of 4 and >= num_kv_heads * block_size");
+    }
+    return VCPP_OK;
+}
+
+}  // namespace
+
+// ---- v1 shims: library-owned buffers ---------------------------------------
+
+namespace {
+// Library-owned device buffers of the v1 entry points (grown, never shrunk).
+struct V1State {
+    std::mutex mu;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    int32_t* ctx = nullptr;
+    size_t ctx_count = 0;
+};
+V1State& v1_state() {
+    static V1State s;
+    return s;
+}
+}  // namespace
+
+
+extern "C" {
+
+const char* vcpp_last_error(void) { return g_last_error.c_str(); }
+
+const char* vcpp_version(void) { return "vcpp_attn 0.1 gfx950"; }
+
+int32_t vcpp_decode_default_partition(int32_t, int32_t, int32_t) { return kDefaultPartition; }
+
+size_t vcpp_decode_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t head_dim,
+                                  int32_t max_context_len, int32_t partition_size) {
+    const int32_t P = resolve_partition(partition_size);
+    return decode_ws_bytes(num_seqs, num_heads, head_dim, num_parts(max_context_len, P));
+}
+
+int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
+                      const int32_t* block_tables, int32_t max_blocks_per_seq,
+                      const int32_t* table_lens, const int32_t* context_lens, int32_t num_seqs,
+                      int32_t max_context_len, int32_t num_heads, int32_t partition_size,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+    g_last_error.clear();
+    int rc = check_pages(kv);
+    if (rc != VCPP_OK) return rc;
+    if (num_seqs < 0) return fail(VCPP_E_INVALID, "num_seqs must be >= 0");
+    if (num_seqs == 0) return VCPP_OK;
+    if (!q || !out || !context_lens) return fail(VCPP_E_INVALID, "q/out/context_lens is NULL");
+    if (max_blocks_per_seq < 0) return fail(VCPP_E_INVALID, "max_blocks_per_seq must be >= 0");
+    if (max_blocks_per_seq > 0 && !block_tables)
+        return fail(VCPP_E_INVALID, "block_tables is NULL");
+    if (num_heads <= 0 || num_heads % kv->num_kv_heads != 0)
+        return fail(VCPP_E_INVALID, "num_heads %d is not a positive multiple of num_kv_heads %d",
+                    num_heads, kv->num_kv_heads);
+    if (max_context_len < 0) return fail(VCPP_E_INVALID, "max_context_len must be >= 0");
+    const int32_t P = resolve_partition(partition_size);
+    if (P % 32 != 0 || P > kMaxPartition)
+        return fail(VCPP_E_INVALID, "partition_size %d must be a multiple of 32 and <= %d", P,
+                    kMaxPartition);
+    const int32_t parts = num_parts(max_context_len, P);
+    if (parts > 65535) return fail(VCPP_E_UNSUPPORTED, "too many partitions (%d)", parts);
+    const size_t need = decode_ws_bytes(num_seqs, num_heads, kv->head_dim, parts);
+    if (need > 0 && (!workspace || workspace_bytes < need))
+        return fail(VCPP_E_WORKSPACE, "decode needs %zu workspace bytes, got %zu", need,
+                    workspace ? workspace_bytes : (size_t)0);
+
+    vcpp::DecodeParams p{};
+    p.k = kv->k;
+    p.v = kv->v;
+    p.k_scale = kv->k_scale;
+    p.v_scale = kv->v_scale;
+    p.num_blocks = kv->num_blocks;
+    p.block_stride = kv->block_stride;
+    p.scale_block_stride = kv->scale_block_stride;
+    p.block_size = kv->block_size;
+    p.num_kv_heads = kv->num_kv_heads;
+    p.head_dim = kv->head_dim;
+    p.kv_dtype = kv->dtype;
+    p.q = q;
+    p.out = out;
+    p.num_heads = num_heads;
+    p.num_seqs = num_seqs;
+    p.group = num_heads / kv->num_kv_heads;
+    p.qchunks = (p.group + 7) / 8;
+    p.pairs = kv->num_kv_heads * p.qchunks;
+    p.block_tables = block_tables;
+    p.table_lens = table_lens;
+    p.context_lens = context_lens;
+    p.max_blocks = max_blocks_per_seq;
+    p.partition = P;
+    p.max_parts = parts;
+    if (need > 0) {
+        const size_t rows = (size_t)num_seqs * parts * num_heads;
+        const size_t o_bytes = ((rows * kv->head_dim * sizeof(float)) + 255) & ~size_t(255);
+        p.ws_o = static_cast<float*>(workspace);
+        p.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + o_bytes);
+    }
+    p.scale_log2 = (1.0f / std::sqrt((float)kv->head_dim)) * 1.4426950408889634f;
+    if (p.pairs > 65535 * 8) return fail(VCPP_E_UNSUPPORTED, "too many kv heads");
+    hipError_t e = vcpp::launch_decode(p, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "decode launch");
+    return VCPP_OK;
+}
+
+void paged_attention_cuda(const float* q, const uint16_t* kv_cache, const int32_t* block_tables,
+                          const int32_t* context_lens, float* out, int32_t num_heads,
+                          int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                          int32_t batch_size) {
+    g_last_error.clear();
+    if (block_size != 16 && block_size != 32) {
+        fail(VCPP_E_UNSUPPORTED, "paged_attention_cuda: block_size %d (only 16 and 32)",
+             block_size);
+        return;
+    }
+    if (batch_size <= 0) return;
+    if (!context_lens) {
+        fail(VCPP_E_INVALID, "paged_attention_cuda: context_lens is NULL");
+        return;
+    }
+    // Host read of the lengths, as cuda/attention.cu:25-28 does.
+    int32_t max_ctx = 0;
+    for (int32_t b = 0; b < batch_size; b++) max_ctx = context_lens[b] > max_ctx ? context_lens[b] : max_ctx;
+    const int32_t max_blocks = max_ctx > 0 ? (max_ctx + block_size - 1) / block_size : 0;
+
+    vcpp_kv_pages kv{};
+    kv.dtype = VCPP_KV_F16;
+    kv.block_size = block_size;
+    kv.num_kv_heads = num_kv_heads;
+    kv.head_dim = head_dim;
+    kv.num_blocks = INT32_MAX;  // not passed by v1: block ids are trusted
+    const int64_t page = (int64_t)block_size * num_kv_heads * head_dim;
+    kv.block_stride = 2 * page;
+    kv.k = kv_cache;
+    kv.v = kv_cache ? kv_cache + page : nullptr;
+
+    V1State& st = v1_state();
+    std::lock_guard<std::mutex> lock(st.mu);
+    const int32_t P = resolve_partition(0);
+    const size_t need =
+        decode_ws_bytes(batch_size, num_heads, head_dim, num_parts(max_ctx, P));
+    if (need > st.ws_bytes) {
+        if (st.ws) (void)hipFree(st.ws);
+        st.ws = nullptr;
+        st.ws_bytes = 0;
+        if (hipMalloc(&st.ws, need) != hipSuccess) {
+            fail(VCPP_E_HIP, "paged_attention_cuda: workspace allocation of %zu bytes", need);
+            return;
+        }
+        st.ws_bytes = need;
+    }
+    if ((size_t)batch_size > st.ctx_count) {
+        if (st.ctx) (void)hipFree(st.ctx);
+        st.ctx = nullptr;
+        st.ctx_count = 0;
+        if (hipMalloc(&st.ctx, sizeof(int32_t) * batch_size) != hipSuccess) {
+            fail(VCPP_E_HIP, "paged_attention_cuda: context_lens staging allocation");
+            return;
+        }
+        st.ctx_count = batch_size;
+    }
+    hipError_t e = hipMemcpyAsync(st.ctx, context_lens, sizeof(int32_t) * batch_size,
+                                  hipMemcpyHostToDevice, nullptr);
+    if (e != hipSuccess) {
+        hip_fail(e, "paged_attention_cuda: context_lens copy");
+        return;
+    }
+    vcpp_paged_decode(&kv, q, out, block_tables, max_blocks, nullptr, st.ctx, batch_size,
+                      max_ctx, num_heads, 0, st.ws, st.ws_bytes, nullptr);
+}
+
+}  // extern "C"

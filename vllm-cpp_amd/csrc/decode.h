@@ -1,0 +1,49 @@
+// decode.h -- internal launch interface of the decode kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vcpp_attention.h"
+
+namespace vcpp {
+
+// Everything a decode launch needs, passed to the kernels by value.
+struct DecodeParams {
+    // KV pages (see vcpp_kv_pages)
+    const void* k;
+    const void* v;
+    const uint16_t* k_scale;
+    const uint16_t* v_scale;
+    int64_t num_blocks;
+    int64_t block_stride;
+    int64_t scale_block_stride;
+    int32_t block_size;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t kv_dtype;
+    // queries / outputs
+    const float* q;
+    float* out;
+    int32_t num_heads;
+    int32_t num_seqs;
+    int32_t group;    // num_heads / num_kv_heads
+    int32_t qchunks;  // ceil(group / 8)
+    int32_t pairs;    // num_kv_heads * qchunks (waves per (partition, seq))
+    // tables
+    const int32_t* block_tables;
+    const int32_t* table_lens;
+    const int32_t* context_lens;
+    int32_t max_blocks;
+    // split-K
+    int32_t partition;
+    int32_t max_parts;
+    float* ws_o;     // [num_seqs][max_parts][num_heads][head_dim]
+    float2* ws_ml;   // [num_seqs][max_parts][num_heads] (max in log2 units, sum)
+    float scale_log2;  // log2(e) / sqrt(head_dim)
+};
+
+hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);
+bool decode_head_dim_supported(int kv_dtype, int head_dim);
+
+}  // namespace vcpp

@@ -1,0 +1,136 @@
+"""ctypes binding of libvcpp_attn.so (include/vcpp_attention.h).
+
+Tests and bench.py call the library only through this module, i.e. through
+the C ABI.  Torch tensors are used as device-memory plumbing (data_ptr() and
+the current HIP stream); nothing here computes attention.  Loading fails
+loudly when the library has not been built -- there is no fallback path.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libvcpp_attn.so")
+
+VCPP_OK = 0
+VCPP_E_INVALID = -1
+VCPP_E_UNSUPPORTED = -2
+VCPP_E_WORKSPACE = -3
+VCPP_E_HIP = -4
+
+KV_F32 = 0
+KV_F16 = 1
+KV_I8 = 2
+
+# Every symbol include/vcpp_attention.h declares.
+EXPORTS = [
+    "vcpp_last_error",
+    "vcpp_version",
+    "vcpp_paged_decode",
+    "vcpp_decode_workspace_size",
+    "vcpp_decode_default_partition",
+    "paged_attention_cuda",
+]
+
+
+class KVPages(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("block_size", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("num_blocks", ctypes.c_int64),
+        ("block_stride", ctypes.c_int64),
+        ("scale_block_stride", ctypes.c_int64),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("k_scale", ctypes.c_void_p),
+        ("v_scale", ctypes.c_void_p),
+    ]
+
+
+class VcppError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__("vcpp error %d: %s" % (code, msg))
+        self.code = code
+
+
+_lib = None
+
+
+def lib():
+    """Loads libvcpp_attn.so once; raises if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            "libvcpp_attn.so not built (%s); run __graft_entry__.build()" % LIB_PATH)
+    L = ctypes.CDLL(LIB_PATH)
+    L.vcpp_last_error.restype = ctypes.c_char_p
+    L.vcpp_version.restype = ctypes.c_char_p
+    vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
+    L.vcpp_paged_decode.argtypes = [ctypes.POINTER(KVPages), vp, vp, vp, i32, vp, vp, i32, i32,
+                                    i32, i32, vp, sz, vp]
+    L.vcpp_paged_decode.restype = ctypes.c_int
+    L.vcpp_decode_workspace_size.argtypes = [i32, i32, i32, i32, i32]
+    L.vcpp_decode_workspace_size.restype = sz
+    L.vcpp_decode_default_partition.argtypes = [i32, i32, i32]
+    L.vcpp_decode_default_partition.restype = i32
+    L.paged_attention_cuda.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32]
+    L.paged_attention_cuda.restype = None
+    _lib = L
+    return L
+
+
+def last_error():
+    return lib().vcpp_last_error().decode()
+
+
+def _check(rc):
+    if rc != VCPP_OK:
+        raise VcppError(rc, last_error())
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def kv_pages(dtype, k, v, block_size, num_kv_heads, head_dim, num_blocks, block_stride,
+             k_scale=None, v_scale=None, scale_block_stride=0):
+    """Builds a vcpp_kv_pages descriptor from device tensors (kept alive by caller)."""
+    return KVPages(dtype, block_size, num_kv_heads, head_dim, num_blocks, block_stride,
+                   scale_block_stride, k.data_ptr(), v.data_ptr(),
+                   None if k_scale is None else k_scale.data_ptr(),
+                   None if v_scale is None else v_scale.data_ptr())
+
+
+def decode_workspace_size(num_seqs, num_heads, head_dim, max_context_len, partition_size=0):
+    return lib().vcpp_decode_workspace_size(num_seqs, num_heads, head_dim, max_context_len,
+                                            partition_size)
+
+
+def paged_decode(pages, q, out, block_tables, context_lens, max_context_len, num_heads,
+                 table_lens=None, partition_size=0, workspace=None, stream=None):
+    """vcpp_paged_decode on device tensors.  `workspace` is a uint8 device tensor
+    of at least decode_workspace_size(...) bytes (allocated here when None)."""
+    num_seqs = q.shape[0]
+    max_blocks = block_tables.shape[1] if block_tables is not None and block_tables.dim() == 2 else 0
+    need = decode_workspace_size(num_seqs, num_heads, pages.head_dim, max_context_len,
+                                 partition_size)
+    if workspace is None and need > 0:
+        import torch
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_bytes = workspace.numel() if workspace is not None else 0
+    rc = lib().vcpp_paged_decode(ctypes.byref(pages), _ptr(q), _ptr(out), _ptr(block_tables),
+                                 max_blocks, _ptr(table_lens), _ptr(context_lens), num_seqs,
+                                 max_context_len, num_heads, partition_size, _ptr(workspace),
+                                 ws_bytes, _stream(stream))
+    _check(rc)
+    return out
