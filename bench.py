@@ -1,0 +1,212 @@
+"""Benchmark of the MI355X paged-attention path (one JSON line on stdout).
+
+Headline (BASELINE.json metric, config 2): batched paged decode attention,
+64 sequences with context lengths uniform in [128, 4096], 64 query heads /
+8 KV heads, head_dim 80, fp16 K/V pages of 16 tokens scattered through a pool
+of 1.25x the tokens, fp32 q/out.  One "step" = one vcpp_paged_decode call over
+the whole batch (decode kernel + split-K merge).  Three independent pools are
+rotated so the 256 MB Infinity Cache cannot serve a step from the previous one.
+
+value = algorithmic bytes per step / measured step time, in TB/s, with every
+input resident in HBM.  Algorithmic bytes = K and V pages of every context
+token (2 * Hkv * D * 2 B per token) + q and out (fp32) + block-table entries.
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20]
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "vllm-cpp_amd"))
+
+HBM_PEAK_TBS = 8.0          # MI355X HBM3E, TB/s
+F16_MFMA_PEAK_TFS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
+
+H, HKV, D, BS = 64, 8, 80, 16
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="target CPU time of the baseline sample")
+    ap.add_argument("--partition", type=int, default=0,
+                    help="split-K partition size (0 = library default)")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# decode workload (config 2)
+
+def decode_workload(torch, seed, pools=3):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    num_seqs = 64
+    ctx = torch.randint(128, 4097, (num_seqs,), generator=g, dtype=torch.int32)
+    total = int(ctx.sum())
+    nb = math.ceil(1.25 * total / BS)
+    nblk = [(int(c) + BS - 1) // BS for c in ctx]
+    max_blocks = max(nblk)
+    dev = torch.device("cuda:0")
+    gd = torch.Generator(device=dev).manual_seed(seed + 1)
+    sets = []
+    for i in range(pools):
+        k = torch.randn((nb, BS, HKV, D), generator=gd, device=dev, dtype=torch.float32).half()
+        v = torch.randn((nb, BS, HKV, D), generator=gd, device=dev, dtype=torch.float32).half()
+        perm = torch.randperm(nb, generator=g)
+        tables = torch.full((num_seqs, max_blocks), -1, dtype=torch.int32)
+        off = 0
+        for s, n in enumerate(nblk):
+            tables[s, :n] = perm[off:off + n]
+            off += n
+        sets.append((k, v, tables.to(dev)))
+    q = torch.randn((num_seqs, H, D), generator=gd, device=dev, dtype=torch.float32)
+    out = torch.empty_like(q)
+    bytes_per_step = (total * 2 * HKV * D * 2          # K and V pages (fp16)
+                      + num_seqs * H * D * (4 + 4)     # q in, out
+                      + sum(nblk) * 4)                 # block-table entries
+    return dict(ctx=ctx, ctx_dev=ctx.to(dev), nb=nb, sets=sets, q=q, out=out,
+                max_ctx=int(ctx.max()), bytes=bytes_per_step, total_tokens=total, nblk=nblk)
+
+
+def run_decode_steps(torch, pyvcpp, w, steps, workspace, partition=0):
+    pages = [pyvcpp.kv_pages(pyvcpp.KV_F16, k, v, BS, HKV, D, w["nb"], BS * HKV * D)
+             for k, v, _ in w["sets"]]
+    for i in range(steps):
+        j = i % len(pages)
+        pyvcpp.paged_decode(pages[j], w["q"], w["out"], w["sets"][j][2], w["ctx_dev"],
+                            w["max_ctx"], H, workspace=workspace, partition_size=partition)
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the reference's own paged_attention() (oracle/_ref, built
+# from the reference sources), single-threaded, over a bounded sample of the
+# same batch (an FP32 pool holding the decoded fp16 values: identical math).
+
+def cpu_baseline(torch, w, target_s):
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    kind = "reference" if O.ref_available() else "port"
+    k, v, tables = w["sets"][0]
+    tables = tables.cpu().numpy()
+    ctx = w["ctx"].numpy().astype(np.int32)
+    q = w["q"].cpu().numpy()
+    kf = k.float().cpu().numpy()
+    vf = v.float().cpu().numpy()
+    if kind == "reference":
+        pool = O.RefPool(kf, vf, fp16=False)
+        cores = 1
+        run = lambda: pool.decode(q, tables, ctx, H)
+    else:
+        pool = O.Pool(O.ORC_F32, kf, vf)
+        cores = os.cpu_count() or 1
+        run = lambda: O.decode(pool, q, tables, ctx, H, nthreads=cores)
+    # whole config-2 batches, repeated until about target_s of CPU time
+    reps, dt = 0, 0.0
+    while dt < target_s and reps < 1000:
+        t0 = time.perf_counter()
+        run()
+        dt += time.perf_counter() - t0
+        reps += 1
+    return {"value": reps * w["bytes"] / dt / 1e12, "unit": "TB/s", "cores": cores, "kind": kind,
+            "sample": "the full config-2 batch (64 seqs, %d context tokens) x %d repetitions, "
+                      "paged_attention() per sequence on an FP32 pool holding the decoded fp16 "
+                      "values, %.1f s" % (w["total_tokens"], reps, dt)}
+
+
+def read_traffic(name):
+    """HBM bytes per launch recorded in profiles/<name> (rocprofv3 --pmc
+    FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration)."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py: this build runs on one GPU only (the paged-attention path has no "
+              "multi-GPU leg here); got --gpus %d" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import pyvcpp
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    pyvcpp.lib()
+
+    w = decode_workload(torch, args.seed)
+    pages0 = pyvcpp.kv_pages(pyvcpp.KV_F16, w["sets"][0][0], w["sets"][0][1], BS, HKV, D, w["nb"],
+                             BS * HKV * D)
+    need = pyvcpp.decode_workspace_size(pages0, 64, H, w["max_ctx"], args.partition)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda:0")
+
+    run_decode_steps(torch, pyvcpp, w, args.warmup, ws, args.partition)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run_decode_steps(torch, pyvcpp, w, args.steps, ws, args.partition)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms_per_step = dt * 1e3 / args.steps
+    value = w["bytes"] / (dt / args.steps) / 1e12
+
+    # Same steps again with per-kernel HIP events on the launch stream.
+    pyvcpp.profile_enable(True)
+    run_decode_steps(torch, pyvcpp, w, args.steps, ws, args.partition)
+    torch.cuda.synchronize()
+    dec_ms, dec_n = pyvcpp.profile_read(pyvcpp.KERNEL_DECODE)
+    mrg_ms, mrg_n = pyvcpp.profile_read(pyvcpp.KERNEL_MERGE)
+    pyvcpp.profile_enable(False)
+    dec_avg_s = dec_ms / max(dec_n, 1) / 1e3
+    achieved = w["bytes"] / dec_avg_s / 1e12
+
+    result = {
+        "metric": "decode attn HBM TB/s (% of peak) + prefill attn TFLOP/s (% fp16 MFMA)",
+        "value": round(value, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 KV / fp32 q,out, fp32 accumulate",
+        "data": "synthetic (seeded N(0,1) q/K/V, random block tables)",
+        "config": {"workload": "BASELINE config 2: batched paged decode, 64 seqs, ctx U[128,4096], "
+                               "64 q / 8 kv heads, head_dim 80, fp16 pages of 16 tokens, pool 1.25x",
+                   "num_seqs": 64, "context_tokens": w["total_tokens"],
+                   "bytes_per_step": w["bytes"], "pool_rotation": len(w["sets"])},
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_TBS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved * 1e3, 1), "peak": HBM_PEAK_TBS * 1e3,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_TBS, 4),
+                     "traffic": read_traffic("decode_mfma_config2_traffic.txt"),
+                     "kernel": "decode_mfma_kernel<f16,80>",
+                     "kernel_avg_us": round(dec_avg_s * 1e6, 2),
+                     "merge_avg_us": round(mrg_ms / max(mrg_n, 1) * 1e3, 2)},
+        "prefill": None,
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(torch, w, args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -94,11 +94,14 @@ typedef struct vcpp_kv_pages {
  *   max_context_len  host-side upper bound of context_lens (sizes the grid;
  *                a larger context_len is an error the kernel cannot report:
  *                positions past max_context_len are not attended)
- *   partition_size   tokens per split-K partition (multiple of 32, <= 1024;
- *                0 = library default).  Sequences longer than one partition
- *                are reduced by a log-sum-exp merge kernel.
+ *   partition_size   0 (default): the tiles of all sequences are split
+ *                evenly over the workgroups the GPU holds at once (fp16/int8)
+ *                or into 256-token partitions (fp32).  > 0 (a multiple of 16,
+ *                <= 1024): about that many tokens per workgroup range or
+ *                partition -- a tuning and test knob.  Ranges that end inside a
+ *                sequence leave partials, merged by a log-sum-exp kernel.
  *   workspace    device scratch of at least vcpp_decode_workspace_size(...)
- *                bytes (may be NULL when that size is 0).
+ *                bytes (may be NULL when that size is 0).  Overwritten.
  * Replaces the per-request loop around paged_attention()
  * (src/paged_engine.cpp:505-508, src/paged_attention.cpp:96-121).
  */
@@ -109,12 +112,10 @@ int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
                       int32_t partition_size, void* workspace, size_t workspace_bytes,
                       void* stream);
 
-size_t vcpp_decode_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t head_dim,
+/* Workspace bytes vcpp_paged_decode needs for these arguments on the current
+ * device (the split depends on its compute-unit count). */
+size_t vcpp_decode_workspace_size(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_heads,
                                   int32_t max_context_len, int32_t partition_size);
-
-/* Partition size the library uses when partition_size == 0. */
-int32_t vcpp_decode_default_partition(int32_t num_seqs, int32_t num_kv_heads,
-                                      int32_t max_context_len);
 
 /* ---- v1: reference launcher signatures (cuda/attention.h) -------------- */
 
@@ -135,6 +136,21 @@ void paged_attention_cuda(const float* q, const uint16_t* kv_cache, const int32_
                           const int32_t* context_lens, float* out, int32_t num_heads,
                           int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                           int32_t batch_size);
+
+/* ---- instrumentation (no reference counterpart) --------------------------- */
+
+/* Kernel ids for vcpp_profile_read. */
+#define VCPP_KERNEL_DECODE 0  /* decode attention (fp16/int8 MFMA or fp32) */
+#define VCPP_KERNEL_MERGE 1   /* split-K log-sum-exp merge */
+#define VCPP_KERNEL_PREFILL 2 /* chunked causal prefill */
+
+/* Start (on != 0) or stop per-kernel timing and clear the counters.  While on,
+ * each launch records a HIP event before and after the kernel on the stream
+ * it is launched on. */
+int vcpp_profile_enable(int on);
+/* Total milliseconds and launch count of one kernel since the last enable;
+ * waits for the recorded events. */
+int vcpp_profile_read(int kernel_id, double* total_ms, int64_t* launches);
 
 #ifdef __cplusplus
 }

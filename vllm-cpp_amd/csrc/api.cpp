@@ -8,6 +8,7 @@
 
 #include <cmath>
 #include <cstdarg>
+#include <algorithm>
 #include <cstdio>
 #include <mutex>
 #include <string>
@@ -36,23 +37,78 @@ int hip_fail(hipError_t e, const char* what) {
 
 constexpr int32_t kDefaultPartition = 256;
 constexpr int32_t kMaxPartition = 1024;
+// fp16/int8 split: at least one 64-token step per range; grid.x limit.
+constexpr int64_t kMinTilesPerRange = 4;
+constexpr int64_t kMaxRanges = 1 << 20;
 
 int32_t ceil_div(int64_t a, int64_t b) { return (int32_t)((a + b - 1) / b); }
-
-int32_t resolve_partition(int32_t partition_size) {
-    return partition_size > 0 ? partition_size : kDefaultPartition;
-}
 
 int32_t num_parts(int32_t max_context_len, int32_t partition) {
     return max_context_len <= 0 ? 1 : ceil_div(max_context_len, partition);
 }
 
-size_t decode_ws_bytes(int32_t num_seqs, int32_t num_heads, int32_t head_dim, int32_t parts) {
-    if (parts <= 1) return 0;
-    const size_t rows = (size_t)num_seqs * parts * num_heads;
-    // o partials, then (m, l) pairs; both 256-byte aligned.
-    const size_t o_bytes = ((rows * head_dim * sizeof(float)) + 255) & ~size_t(255);
-    return o_bytes + ((rows * sizeof(float2) + 255) & ~size_t(255));
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// Launch geometry and workspace layout of one decode call.
+struct DecodePlan {
+    int32_t num_wg = 0;      // fp16/int8: workgroup ranges per kv-head group
+    int32_t partition = 0;   // fp32: tokens per partition
+    int32_t max_parts = 0;   // fp32: partitions per sequence
+    size_t off_tile_start = 0, off_first_seq = 0, off_o = 0, off_ml = 0, bytes = 0;
+};
+
+DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_heads,
+                       int32_t max_context_len, int32_t partition_size) {
+    DecodePlan pl;
+    const int D = kv->head_dim;
+    if (kv->dtype == VCPP_KV_F32) {
+        pl.partition = partition_size > 0 ? partition_size : kDefaultPartition;
+        pl.max_parts = num_parts(max_context_len, pl.partition);
+        if (pl.max_parts > 1) {
+            const size_t rows = (size_t)num_seqs * pl.max_parts * num_heads;
+            pl.off_o = 0;
+            pl.off_ml = align256(rows * D * sizeof(float));
+            pl.bytes = pl.off_ml + align256(rows * sizeof(float2));
+        }
+        return pl;
+    }
+    const int group = num_heads / kv->num_kv_heads;
+    const int pairs = kv->num_kv_heads * ((group + 7) / 8);
+    const int wpw = pairs < 4 ? pairs : 4;
+    const int groups = vcpp::decode_group_count(pairs);
+    // Ranges that are all resident at once: 2 waves per SIMD, 4 SIMDs per CU.
+    const int64_t slots = (int64_t)device_cus() * (8 / wpw);
+    int64_t G = slots / groups;
+    const int64_t tiles_upper = (int64_t)num_seqs * ((max_context_len + 15) / 16);
+    if (partition_size > 0) {
+        G = (tiles_upper * 16 + partition_size - 1) / partition_size;
+    } else {
+        G = std::min<int64_t>(G, (tiles_upper + kMinTilesPerRange - 1) / kMinTilesPerRange);
+    }
+    G = std::max<int64_t>(1, std::min<int64_t>(G, kMaxRanges));
+    pl.num_wg = (int32_t)G;
+    pl.off_tile_start = 0;
+    pl.off_first_seq = align256(sizeof(int32_t) * ((size_t)num_seqs + 1));
+    pl.off_o = pl.off_first_seq + align256(sizeof(int32_t) * (size_t)G);
+    const size_t rows = (size_t)G * 2 * num_heads;
+    pl.off_ml = pl.off_o + align256(rows * D * sizeof(float));
+    pl.bytes = pl.off_ml + align256(rows * sizeof(float2));
+    return pl;
 }
 
 int check_pages(const vcpp_kv_pages* kv) {
@@ -64,7 +120,7 @@ int check_pages(const vcpp_kv_pages* kv) {
                     kv->block_size);
     if (kv->num_kv_heads <= 0) return fail(VCPP_E_INVALID, "num_kv_heads must be positive");
     if (kv->num_blocks < 0) return fail(VCPP_E_INVALID, "num_blocks must be >= 0");
-    if (!vcpp::decode_head_dim_supported(kv->dtype, kv->head_dim))
+    if (kv->head_dim > 256 || !vcpp::decode_head_dim_supported(kv->dtype, kv->head_dim))
         return fail(VCPP_E_UNSUPPORTED, "head_dim %d not supported for kv dtype %d",
                     kv->head_dim, kv->dtype);
     if (kv->num_blocks > 0 && (!kv->k || !kv->v))
@@ -119,12 +175,10 @@ const char* vcpp_last_error(void) { return g_last_error.c_str(); }
 
 const char* vcpp_version(void) { return "vcpp_attn 0.1 gfx950"; }
 
-int32_t vcpp_decode_default_partition(int32_t, int32_t, int32_t) { return kDefaultPartition; }
-
-size_t vcpp_decode_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t head_dim,
+size_t vcpp_decode_workspace_size(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_heads,
                                   int32_t max_context_len, int32_t partition_size) {
-    const int32_t P = resolve_partition(partition_size);
-    return decode_ws_bytes(num_seqs, num_heads, head_dim, num_parts(max_context_len, P));
+    if (!kv || kv->num_kv_heads <= 0 || num_heads <= 0 || num_seqs <= 0) return 0;
+    return plan_decode(kv, num_seqs, num_heads, max_context_len, partition_size).bytes;
 }
 
 int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
@@ -145,13 +199,12 @@ int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
         return fail(VCPP_E_INVALID, "num_heads %d is not a positive multiple of num_kv_heads %d",
                     num_heads, kv->num_kv_heads);
     if (max_context_len < 0) return fail(VCPP_E_INVALID, "max_context_len must be >= 0");
-    const int32_t P = resolve_partition(partition_size);
-    if (P % 32 != 0 || P > kMaxPartition)
-        return fail(VCPP_E_INVALID, "partition_size %d must be a multiple of 32 and <= %d", P,
-                    kMaxPartition);
-    const int32_t parts = num_parts(max_context_len, P);
-    if (parts > 65535) return fail(VCPP_E_UNSUPPORTED, "too many partitions (%d)", parts);
-    const size_t need = decode_ws_bytes(num_seqs, num_heads, kv->head_dim, parts);
+    if (partition_size < 0 || partition_size % 16 != 0 || partition_size > kMaxPartition)
+        return fail(VCPP_E_INVALID, "partition_size %d must be 0 or a multiple of 16 <= %d",
+                    partition_size, kMaxPartition);
+    const DecodePlan pl = plan_decode(kv, num_seqs, num_heads, max_context_len, partition_size);
+    if (pl.max_parts > 65535) return fail(VCPP_E_UNSUPPORTED, "too many partitions (%d)", pl.max_parts);
+    const size_t need = pl.bytes;
     if (need > 0 && (!workspace || workspace_bytes < need))
         return fail(VCPP_E_WORKSPACE, "decode needs %zu workspace bytes, got %zu", need,
                     workspace ? workspace_bytes : (size_t)0);
@@ -179,13 +232,16 @@ int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
     p.table_lens = table_lens;
     p.context_lens = context_lens;
     p.max_blocks = max_blocks_per_seq;
-    p.partition = P;
-    p.max_parts = parts;
+    char* ws = static_cast<char*>(workspace);
+    p.partition = pl.partition;
+    p.max_parts = pl.max_parts;
+    p.num_wg = pl.num_wg;
+    p.ctx_cap = max_context_len;
     if (need > 0) {
-        const size_t rows = (size_t)num_seqs * parts * num_heads;
-        const size_t o_bytes = ((rows * kv->head_dim * sizeof(float)) + 255) & ~size_t(255);
-        p.ws_o = static_cast<float*>(workspace);
-        p.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + o_bytes);
+        p.tile_start = reinterpret_cast<int32_t*>(ws + pl.off_tile_start);
+        p.first_seq = reinterpret_cast<int32_t*>(ws + pl.off_first_seq);
+        p.ws_o = reinterpret_cast<float*>(ws + pl.off_o);
+        p.ws_ml = reinterpret_cast<float2*>(ws + pl.off_ml);
     }
     p.scale_log2 = (1.0f / std::sqrt((float)kv->head_dim)) * 1.4426950408889634f;
     if (p.pairs > 65535 * 8) return fail(VCPP_E_UNSUPPORTED, "too many kv heads");
@@ -227,9 +283,7 @@ void paged_attention_cuda(const float* q, const uint16_t* kv_cache, const int32_
 
     V1State& st = v1_state();
     std::lock_guard<std::mutex> lock(st.mu);
-    const int32_t P = resolve_partition(0);
-    const size_t need =
-        decode_ws_bytes(batch_size, num_heads, head_dim, num_parts(max_ctx, P));
+    const size_t need = plan_decode(&kv, batch_size, num_heads, max_ctx, 0).bytes;
     if (need > st.ws_bytes) {
         if (st.ws) (void)hipFree(st.ws);
         st.ws = nullptr;

@@ -35,15 +35,24 @@ struct DecodeParams {
     const int32_t* table_lens;
     const int32_t* context_lens;
     int32_t max_blocks;
-    // split-K
+    // fp16/int8: balanced split of the concatenated 16-token tiles over
+    // num_wg workgroup ranges (per kv-head group)
+    int32_t num_wg;
+    int32_t ctx_cap;       // context lengths are clamped to this
+    int32_t* tile_start;   // [num_seqs + 1] exclusive prefix of tiles per sequence
+    int32_t* first_seq;    // [num_wg] sequence holding each range's first tile
+    // fp32: fixed partitions of `partition` tokens, max_parts per sequence
     int32_t partition;
     int32_t max_parts;
-    float* ws_o;     // [num_seqs][max_parts][num_heads][head_dim]
-    float2* ws_ml;   // [num_seqs][max_parts][num_heads] (max in log2 units, sum)
+    // partials: fp16/int8 [num_wg][2 slots][num_heads], fp32 [num_seqs][max_parts][num_heads]
+    float* ws_o;     // (.., head_dim) unnormalised outputs
+    float2* ws_ml;   // (max in log2 units, sum of exponentials)
     float scale_log2;  // log2(e) / sqrt(head_dim)
 };
 
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);
+// Workgroups along y of the fp16/int8 grid (kv-head groups of up to 4 waves).
+int decode_group_count(int pairs);
 bool decode_head_dim_supported(int kv_dtype, int head_dim);
 
 }  // namespace vcpp

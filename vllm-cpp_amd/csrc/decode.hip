@@ -6,121 +6,152 @@
 // The reference's GPU slot is cuda/attention.cu:11-52; its kernel
 // (cuda/attention_kernels.cuh:9-123) is not followed.
 //
-// Work decomposition: one workgroup per (partition, sequence, kv-head slice);
-// one wave per (kv head, chunk of <= 8 query heads of its GQA group), so every
-// K/V page is read from HBM once for the whole group.  A 16-token tile is one
-// MFMA step:
-//   S^T[16 tok][16] = K_tile[16 tok][D] x Qs^T     (16x16x32 f16 steps)
-//   O[16][D]       += P[16][16 tok] x V_tile        (16x16x16 f16, D/16 tiles)
-// The 16 MFMA rows hold the fp16 "hi" part of the 8 query heads (rows 0-7)
-// and the fp16 residual q - hi (rows 8-15); likewise P = p_hi + p_lo.  Summing
-// the two halves keeps about 22 significant bits of q and p while K/V stay
-// exact fp16, with fp32 accumulation -- the padding rows an 8-head group would
-// waste on a 16-row MFMA carry the low halves instead.
-// V is needed with tokens along the MFMA k dimension, so each wave stages its
-// V tile in LDS (row-major, padded rows) and reads it back transposed.
-// Long contexts are split into partitions; each writes (m, l, o) partials and
-// the log-sum-exp merge kernel combines them.
+// fp16 / int8 pages (the HBM-bound path):
+//  * One wave per (kv head, chunk of <= 8 query heads of its GQA group): every
+//    K/V page is read from HBM once for the whole group.  Workgroups hold 4
+//    waves = 4 kv heads = 640 contiguous bytes of each token row.
+//  * Balanced split: the 16-token tiles of all sequences are laid end to end
+//    and every resident workgroup takes an equal contiguous range of them, so
+//    ragged batches keep the whole GPU busy to the end.  A range touches 1-3
+//    sequences; a sequence wholly inside one range is finished in place, and
+//    at most two fragments per range (the sequence continuing from the
+//    previous range, the one continuing into the next) leave (m, l, o)
+//    partials that a log-sum-exp merge kernel combines.
+//  * A 16-token tile is one MFMA step:
+//      S^T[16 tok][16] = K_tile[16 tok][D] x Qs^T   (16x16x32 f16; a 16-dim
+//                                                    remainder as 16x16x16)
+//      O[16][D]       += P[16][16 tok] x V_tile      (16x16x16 f16)
+//    The 16 MFMA rows hold the fp16 "hi" part of the 8 query heads (rows 0-7)
+//    and the fp16 residual q - hi (rows 8-15); likewise P = p_hi + p_lo, so
+//    q and p keep about 22 significant bits while K/V stay exact fp16, with
+//    fp32 accumulation: the rows an 8-head group would waste carry the low
+//    halves instead.
+//  * K fragments come straight from HBM into registers (one 16-byte buffer
+//    load per lane per 32 dims).  V is staged row-major in LDS and read back
+//    with ds_read_b64_tr_b16, which hands each lane four tokens of one dim --
+//    the P x V operand -- in one instruction.
+//  * Loads go through buffer descriptors sized to the tile (zero-sized for an
+//    invalid block, which then reads as zeros), so every load is issued
+//    unconditionally, two 64-token steps are kept in flight in ping-pong
+//    register buffers and the wait counts stay static.
+// fp32 pages use a plain VALU kernel over fixed partitions (parity path).
 #include "decode.h"
 #include "device_common.h"
+#include "profile.h"
 
 namespace vcpp {
 
 namespace {
 
 constexpr int kTile = 16;          // tokens per MFMA tile
-constexpr int kTilesPerIter = 2;   // tiles per softmax update / prefetch step
+constexpr int kTilesPerIter = 4;   // tiles per softmax update / prefetch step
+// Waves (kv heads) per workgroup: 4 kv heads x 80 dims x 2 B = 640 B, five
+// whole 128-byte lines of every token row.
+constexpr int kWavesPerGroup = 4;
+
+typedef short s4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) char lds_char;
 
 template <int D>
 struct Dims {
-    static constexpr int NC32 = D / 32;         // 16x16x32 steps over head_dim
-    // A trailing 16-dim remainder runs as one more 16x16x32 step whose lane
-    // groups 2-3 carry zeros (padding in registers, not in HBM).  One opcode
-    // per accumulation chain: a 16x16x16 step chained straight after a
-    // 16x16x32 one on the same accumulator was measured to drop the previous
-    // step's contribution on gfx950 with this toolchain.
+    static constexpr int NC32 = D / 32;  // 16x16x32 steps over head_dim
+    // A trailing 16-dim remainder runs as a 16x16x16 step into its own
+    // accumulator.  One opcode per accumulation chain: a 16x16x16 step
+    // chained straight onto a 16x16x32 accumulator was measured to drop the
+    // previous step's contribution on gfx950 with this toolchain.
     static constexpr int REM = (D % 32) / 16;
-    static constexpr int NT = D / 16;           // output 16-column tiles
-    static constexpr int VROW = D + 8;          // LDS row pitch in halves
+    static constexpr int NT = D / 16;    // output 16-column tiles
     static_assert(D % 16 == 0 && D <= 256, "head_dim must be a multiple of 16");
 };
 
-// Registers of one 16-token tile for one lane.
+// Registers of one 16-token tile for one lane (token c, head_dim chunk g).
 template <int KV, int D>
 struct Tile;
 
 template <int D>
 struct Tile<VCPP_KV_F16, D> {
     h8 k[Dims<D>::NC32 > 0 ? Dims<D>::NC32 : 1];
-    h8 kr;  // dims 32*NC32 + 8g.. for lane groups 0-1, zero for 2-3
+    h4 kr;  // dims 32*NC32 + 4g .. +3
     h8 v[Dims<D>::NC32 > 0 ? Dims<D>::NC32 : 1];
-    h8 vr;
+    h4 vr;
 };
 
 template <int D>
 struct Tile<VCPP_KV_I8, D> {
     i2 k[Dims<D>::NC32 > 0 ? Dims<D>::NC32 : 1];
-    i2 kr;
+    uint32_t kr;
     i2 v[Dims<D>::NC32 > 0 ? Dims<D>::NC32 : 1];
-    i2 vr;
+    uint32_t vr;
     i2 ks;  // fp16 K scales of tokens 4g..4g+3
     i2 vs;  // fp16 V scales of tokens 4g..4g+3
 };
 
-template <int KV>
-struct Elem;
-template <>
-struct Elem<VCPP_KV_F16> { typedef _Float16 T; };
-template <>
-struct Elem<VCPP_KV_I8> { typedef int8_t T; };
+// Per-lane byte offsets of the lane's share of a tile, identical for every
+// tile: only the buffer base moves.
+struct LaneOffsets {
+    int k[4];   // 16x16x32 chunks (head_dim <= 128)
+    int rem;    // 16x16x16 remainder chunk
+    int scale;  // int8: fp16 scales of tokens 4g..4g+3
+};
 
-// Loads the lane's share of one tile: token c of the tile, head_dim chunk g.
-// An invalid block yields zeros (its tokens are masked anyway).
+template <int KV, int D>
+__device__ __forceinline__ LaneOffsets lane_offsets(const DecodeParams& p, int kvh, int g, int c) {
+    constexpr int ES = KV == VCPP_KV_F16 ? 2 : 1;
+    LaneOffsets o;
+    const int row = (c * p.num_kv_heads + kvh) * D;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) o.k[cc] = (row + 32 * cc + 8 * g) * ES;
+    o.rem = (row + 32 * Dims<D>::NC32 + 4 * g) * ES;
+    o.scale = (kvh * p.block_size + 4 * g) * 2;
+    return o;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+    // dword3 0x00020000: raw 32-bit data format, the gfx9 setting for untyped
+    // buffer loads; out-of-range offsets read as zero.
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+// Issues the lane's loads of one tile through buffer descriptors whose size is
+// the tile's 16 token rows (and the block's scale page), or zero for an
+// invalid block: the hardware then returns zeros without touching memory.
 template <int KV, int D>
 __device__ __forceinline__ void load_tile(Tile<KV, D>& t, const DecodeParams& p, int bid,
-                                          int tok_in_block, int kvh, int g, int c) {
-    typedef typename Elem<KV>::T E;
+                                          int tok_in_block, const LaneOffsets& lo) {
     constexpr int NC32 = Dims<D>::NC32;
-    if (bid < 0) {
-        t = Tile<KV, D>{};
-        return;
-    }
-    const int64_t row = (int64_t)bid * p.block_stride +
-                        ((int64_t)(tok_in_block + c) * p.num_kv_heads + kvh) * D;
-    const E* kp = reinterpret_cast<const E*>(p.k) + row;
-    const E* vp = reinterpret_cast<const E*>(p.v) + row;
+    constexpr int ES = KV == VCPP_KV_F16 ? 2 : 1;
+    const bool ok = bid >= 0;
+    const int64_t elem = (int64_t)(ok ? bid : 0) * p.block_stride +
+                         (int64_t)tok_in_block * p.num_kv_heads * D;
+    const int bytes = ok ? kTile * p.num_kv_heads * D * ES : 0;
+    const auto kr = make_rsrc(static_cast<const char*>(p.k) + elem * ES, bytes);
+    const auto vr = make_rsrc(static_cast<const char*>(p.v) + elem * ES, bytes);
     if constexpr (KV == VCPP_KV_F16) {
 #pragma unroll
         for (int cc = 0; cc < NC32; ++cc) {
-            t.k[cc] = *reinterpret_cast<const h8*>(kp + 32 * cc + 8 * g);
-            t.v[cc] = *reinterpret_cast<const h8*>(vp + 32 * cc + 8 * g);
+            t.k[cc] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(kr, lo.k[cc], 0, 0));
+            t.v[cc] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(vr, lo.k[cc], 0, 0));
         }
         if constexpr (Dims<D>::REM) {
-            t.kr = h8{};
-            t.vr = h8{};
-            if (g < 2) {
-                t.kr = *reinterpret_cast<const h8*>(kp + 32 * NC32 + 8 * g);
-                t.vr = *reinterpret_cast<const h8*>(vp + 32 * NC32 + 8 * g);
-            }
+            t.kr = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(kr, lo.rem, 0, 0));
+            t.vr = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(vr, lo.rem, 0, 0));
         }
     } else {
 #pragma unroll
         for (int cc = 0; cc < NC32; ++cc) {
-            t.k[cc] = *reinterpret_cast<const i2*>(kp + 32 * cc + 8 * g);
-            t.v[cc] = *reinterpret_cast<const i2*>(vp + 32 * cc + 8 * g);
+            t.k[cc] = __builtin_bit_cast(i2, __builtin_amdgcn_raw_buffer_load_b64(kr, lo.k[cc], 0, 0));
+            t.v[cc] = __builtin_bit_cast(i2, __builtin_amdgcn_raw_buffer_load_b64(vr, lo.k[cc], 0, 0));
         }
         if constexpr (Dims<D>::REM) {
-            t.kr = i2{};
-            t.vr = i2{};
-            if (g < 2) {
-                t.kr = *reinterpret_cast<const i2*>(kp + 32 * NC32 + 8 * g);
-                t.vr = *reinterpret_cast<const i2*>(vp + 32 * NC32 + 8 * g);
-            }
+            t.kr = __builtin_amdgcn_raw_buffer_load_b32(kr, lo.rem, 0, 0);
+            t.vr = __builtin_amdgcn_raw_buffer_load_b32(vr, lo.rem, 0, 0);
         }
-        const int64_t srow = (int64_t)bid * p.scale_block_stride +
-                             (int64_t)kvh * p.block_size + tok_in_block + 4 * g;
-        t.ks = *reinterpret_cast<const i2*>(p.k_scale + srow);
-        t.vs = *reinterpret_cast<const i2*>(p.v_scale + srow);
+        const int64_t se = (int64_t)(ok ? bid : 0) * p.scale_block_stride + tok_in_block;
+        const int sbytes = ok ? (p.num_kv_heads * p.block_size - tok_in_block) * 2 : 0;
+        const auto ksr = make_rsrc(p.k_scale + se, sbytes);
+        const auto vsr = make_rsrc(p.v_scale + se, sbytes);
+        t.ks = __builtin_bit_cast(i2, __builtin_amdgcn_raw_buffer_load_b64(ksr, lo.scale, 0, 0));
+        t.vs = __builtin_bit_cast(i2, __builtin_amdgcn_raw_buffer_load_b64(vsr, lo.scale, 0, 0));
     }
 }
 
@@ -131,257 +162,394 @@ __device__ __forceinline__ h8 k_chunk(const Tile<KV, D>& t, int cc) {
     else return i8x8_to_h8((uint32_t)t.k[cc].x, (uint32_t)t.k[cc].y);
 }
 template <int KV, int D>
-__device__ __forceinline__ h8 k_rem(const Tile<KV, D>& t) {
+__device__ __forceinline__ h4 k_rem(const Tile<KV, D>& t) {
     if constexpr (KV == VCPP_KV_F16) return t.kr;
-    else return i8x8_to_h8((uint32_t)t.kr.x, (uint32_t)t.kr.y);
+    else return i8x4_to_h4(t.kr);
 }
 
-// Writes the lane's V row chunk (token c) into the wave's LDS tile, zeroing
-// rows of masked tokens so 0 * garbage cannot produce NaN in P x V.
+// Writes the lane's V row chunk (token c) into the wave's row-major LDS tile
+// [16 tok][D]; rows of masked tokens are written as zeros so 0 * garbage
+// cannot produce NaN in P x V.
 template <int KV, int D>
-__device__ __forceinline__ void stage_v(_Float16* lds, const Tile<KV, D>& t, bool valid, int g,
+__device__ __forceinline__ void stage_v(lds_char* tile, const Tile<KV, D>& t, bool valid, int g,
                                         int c) {
-    constexpr int NC32 = Dims<D>::NC32, VROW = Dims<D>::VROW;
-    _Float16* row = lds + c * VROW;
+    constexpr int NC32 = Dims<D>::NC32;
+    lds_char* row = tile + c * D * 2;
 #pragma unroll
     for (int cc = 0; cc < NC32; ++cc) {
         h8 x;
         if constexpr (KV == VCPP_KV_F16) x = t.v[cc];
         else x = i8x8_to_h8((uint32_t)t.v[cc].x, (uint32_t)t.v[cc].y);
         if (!valid) x = h8{};
-        *reinterpret_cast<h8*>(row + 32 * cc + 8 * g) = x;
+        *reinterpret_cast<__attribute__((address_space(3))) h8*>(row + (32 * cc + 8 * g) * 2) = x;
     }
     if constexpr (Dims<D>::REM) {
-        h8 x;
+        h4 x;
         if constexpr (KV == VCPP_KV_F16) x = t.vr;
-        else x = i8x8_to_h8((uint32_t)t.vr.x, (uint32_t)t.vr.y);
-        if (!valid) x = h8{};
-        if (g < 2) *reinterpret_cast<h8*>(row + 32 * NC32 + 8 * g) = x;
+        else x = i8x4_to_h4(t.vr);
+        if (!valid) x = h4{};
+        *reinterpret_cast<__attribute__((address_space(3))) h4*>(row + (32 * NC32 + 4 * g) * 2) = x;
     }
+}
+
+// P x V operand of output columns 16t..16t+15: lane (g, c) receives
+// V[4g + r][16t + c], r = 0..3.  ds_read_b64_tr_b16 gives lane i of each
+// 16-lane group element (i mod 4) of the 8-byte read of lane 4j + i/4, so
+// lane (g, c) reads row 4g + c/4, columns 16t + 4(c mod 4) .. +3.
+template <int D>
+__device__ __forceinline__ h4 read_v_tr(lds_char* tile, int t, int g, int c) {
+    lds_char* a = tile + ((4 * g + (c >> 2)) * D + 16 * t + 4 * (c & 3)) * 2;
+    const s4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        reinterpret_cast<__attribute__((address_space(3))) s4*>(a));
+    return __builtin_bit_cast(h4, x);
 }
 
 __device__ __forceinline__ float h_to_f(uint32_t bits16) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }
 
+__device__ __forceinline__ int tiles_of(const DecodeParams& p, int s) {
+    const int ctx = min(max(p.context_lens[s], 0), p.ctx_cap);
+    return (ctx + kTile - 1) / kTile;
+}
+
+// First tile of workgroup range w: floor(w * T / G).
+__device__ __forceinline__ int range_start(int w, int T, int G) {
+    return (int)(((int64_t)w * T) / G);
+}
+
+// ---- scan: tile prefix sums and each workgroup's first sequence -----------
+
+__global__ __launch_bounds__(1024) void split_scan_kernel(DecodeParams p) {
+    __shared__ int wave_sums[16];
+    __shared__ int carry_s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) carry_s = 0;
+    __syncthreads();
+    for (int base = 0; base < p.num_seqs; base += 1024) {
+        const int s = base + tid;
+        const int nt = s < p.num_seqs ? tiles_of(p, s) : 0;
+        int x = nt;
+#pragma unroll
+        for (int k = 1; k < 64; k <<= 1) {
+            const int y = __shfl_up(x, k, 64);
+            if (lane >= k) x += y;
+        }
+        if (lane == 63) wave_sums[wave] = x;
+        __syncthreads();
+        int before = carry_s;
+        for (int w2 = 0; w2 < wave; ++w2) before += wave_sums[w2];
+        if (s < p.num_seqs) p.tile_start[s] = before + x - nt;
+        __syncthreads();
+        if (tid == 1023) carry_s = before + x;
+        __syncthreads();
+    }
+    const int T = carry_s;
+    if (tid == 0) p.tile_start[p.num_seqs] = T;
+    __syncthreads();
+    // first_seq[w] = the sequence holding tile range_start(w) (num_seqs if none).
+    for (int w = tid; w < p.num_wg; w += 1024) {
+        const int a = range_start(w, T, p.num_wg);
+        int lo = 0, hi = p.num_seqs;  // smallest s with tile_start[s + 1] > a
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (p.tile_start[mid + 1] > a) hi = mid;
+            else lo = mid + 1;
+        }
+        p.first_seq[w] = lo;
+    }
+}
+
+// ---- the decode kernel ----------------------------------------------------
+
 template <int KV, int D>
-__global__ __launch_bounds__(512) void decode_mfma_kernel(DecodeParams p) {
-    constexpr int NC32 = Dims<D>::NC32, NT = Dims<D>::NT, VROW = Dims<D>::VROW;
-    extern __shared__ _Float16 lds_all[];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void decode_mfma_kernel(DecodeParams p) {
+    constexpr int NC32 = Dims<D>::NC32, NT = Dims<D>::NT;
+    extern __shared__ char lds_raw[];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int g = lane >> 4, c = lane & 15;
-    const int pair = blockIdx.z * (blockDim.x >> 6) + wave;
-    if (pair >= p.pairs) return;
-    const int seq = blockIdx.y, part = blockIdx.x;
-    const int ctx = min(p.context_lens[seq], p.max_parts * p.partition);
-    const int P = p.partition;
-    const int np = ctx <= 0 ? 1 : min((ctx + P - 1) / P, p.max_parts);
-    if (part >= np) return;
+    const int pair = blockIdx.y * (blockDim.x >> 6) + wave;
+    if (pair >= p.pairs) return;  // whole waves only; no workgroup barriers below
+    const int w = blockIdx.x, G = p.num_wg;
+    const int T = p.tile_start[p.num_seqs];
+    const int a = range_start(w, T, G), b = range_start(w + 1, T, G);
+    if (a >= b) return;
 
     const int kvh = pair / p.qchunks, qc = pair - kvh * p.qchunks;
     const int head_base = kvh * p.group + qc * 8;
     const int gc = min(8, p.group - qc * 8);
-    int tlen = p.max_blocks;
-    if (p.table_lens) tlen = min(tlen, p.table_lens[seq]);
-    const int start = part * P;
-    const int stop = min(start + P, ctx);                          // tokens visited
-    const int end = min(stop, (int)min((int64_t)tlen * p.block_size, (int64_t)INT32_MAX));
-    const int ntiles = stop > start ? (stop - start + kTile - 1) / kTile : 0;
+    const LaneOffsets lofs = lane_offsets<KV, D>(p, kvh, g, c);
+    lds_char* lds = reinterpret_cast<lds_char*>((__attribute__((address_space(3))) char*)lds_raw) +
+                    wave * (kTilesPerIter * kTile * D * 2);
 
-    // Query fragment (B operand): row c = hi (c < 8) or lo (c >= 8) of head c & 7.
-    h8 qa[NC32 > 0 ? NC32 : 1];
-    h8 qr = {};
-    {
-        const bool qv = (c & 7) < gc;
-        const float* qrow = p.q + ((int64_t)seq * p.num_heads + head_base + (c & 7)) * D;
-#pragma unroll
-        for (int cc = 0; cc < NC32; ++cc) {
-            f4 x0 = {}, x1 = {};
-            if (qv) {
-                x0 = *reinterpret_cast<const f4*>(qrow + 32 * cc + 8 * g);
-                x1 = *reinterpret_cast<const f4*>(qrow + 32 * cc + 8 * g + 4);
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                float x = i < 4 ? x0[i] : x1[i - 4];
-                _Float16 hi = (_Float16)x;
-                qa[cc][i] = c < 8 ? hi : (_Float16)(x - (float)hi);
-            }
-        }
-        if constexpr (Dims<D>::REM) {
-            f4 x0 = {}, x1 = {};
-            if (qv && g < 2) {
-                x0 = *reinterpret_cast<const f4*>(qrow + 32 * NC32 + 8 * g);
-                x1 = *reinterpret_cast<const f4*>(qrow + 32 * NC32 + 8 * g + 4);
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                float x = i < 4 ? x0[i] : x1[i - 4];
-                _Float16 hi = (_Float16)x;
-                qr[i] = c < 8 ? hi : (_Float16)(x - (float)hi);
-            }
-        }
-    }
+    for (int s = p.first_seq[w]; s < p.num_seqs; ++s) {
+        const int S = p.tile_start[s], E = p.tile_start[s + 1];
+        if (S >= b) break;
+        if (E <= a) continue;  // zero-tile sequence before the range
+        const int t0 = max(a, S) - S, t1 = min(b, E) - S;
+        const bool complete = S >= a && E <= b;
+        const int slot = S < a ? 0 : 1;
 
-    // Physical block of each tile in the partition (lane j <-> tile j), -1 if
-    // the logical block is past the table or the id is out of range.
-    int my_bid = -1, my_off = 0;
-    if (lane < ntiles) {
-        const int pos = start + lane * kTile;
-        const int lb = pos / p.block_size;
-        my_off = pos - lb * p.block_size;
-        if (lb < tlen) {
-            const int id = p.block_tables[(int64_t)seq * p.max_blocks + lb];
-            if (id >= 0 && (int64_t)id < p.num_blocks) my_bid = id;
-        }
-    }
+        const int ctx = min(max(p.context_lens[s], 0), p.ctx_cap);
+        int tlen = p.max_blocks;
+        if (p.table_lens) tlen = min(tlen, p.table_lens[s]);
+        const int end = (int)min((int64_t)ctx, (int64_t)tlen * p.block_size);
 
-    _Float16* lds = lds_all + wave * (kTilesPerIter * kTile * VROW);
-
-    f4 o[NT];
+        // Query fragment: row c = hi (c < 8) or lo (c >= 8) of head c & 7.
+        h8 qa[NC32 > 0 ? NC32 : 1];
+        h4 qr = {};
+        {
+            const bool qv = (c & 7) < gc;
+            const float* qrow = p.q + ((int64_t)s * p.num_heads + head_base + (c & 7)) * D;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) o[t] = f4{0.f, 0.f, 0.f, 0.f};
-    float m_run = kMaxSeed, l_run = 0.f;
-
-    Tile<KV, D> cur[kTilesPerIter], nxt[kTilesPerIter];
-    const int niters = (ntiles + kTilesPerIter - 1) / kTilesPerIter;
-#pragma unroll
-    for (int j = 0; j < kTilesPerIter; ++j) {
-        const int bid = j < ntiles ? __builtin_amdgcn_readlane(my_bid, j) : -1;
-        const int off = __builtin_amdgcn_readlane(my_off, j & 63);
-        load_tile<KV, D>(cur[j], p, bid, off, kvh, g, c);
-    }
-
-    for (int it = 0; it < niters; ++it) {
-        // Prefetch the next step's tiles while this one computes.
-        if (it + 1 < niters) {
-#pragma unroll
-            for (int j = 0; j < kTilesPerIter; ++j) {
-                const int tt = (it + 1) * kTilesPerIter + j;
-                const int bid = tt < ntiles ? __builtin_amdgcn_readlane(my_bid, tt) : -1;
-                const int off = __builtin_amdgcn_readlane(my_off, tt & 63);
-                load_tile<KV, D>(nxt[j], p, bid, off, kvh, g, c);
-            }
-        }
-
-        float s[kTilesPerIter][4];
-        float mx = kMaxSeed;
-#pragma unroll
-        for (int j = 0; j < kTilesPerIter; ++j) {
-            const int tt = it * kTilesPerIter + j;
-            const int bid = tt < ntiles ? __builtin_amdgcn_readlane(my_bid, tt & 63) : -1;
-            const int pos0 = start + tt * kTile;
-            f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int cc = 0; cc < NC32; ++cc) acc = mfma32(k_chunk<KV, D>(cur[j], cc), qa[cc], acc);
-            if constexpr (Dims<D>::REM) acc = mfma32(k_rem<KV, D>(cur[j]), qr, acc);
-            stage_v<KV, D>(lds + j * kTile * VROW, cur[j], bid >= 0 && pos0 + c < end, g, c);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float x = acc[r] + dpp_ror8(acc[r]);
-                float f = p.scale_log2;
-                if constexpr (KV == VCPP_KV_I8) {
-                    const uint32_t w = (uint32_t)(r < 2 ? cur[j].ks.x : cur[j].ks.y);
-                    f *= h_to_f((r & 1) ? (w >> 16) : (w & 0xFFFFu));
+            for (int cc = 0; cc < NC32; ++cc) {
+                f4 x0 = {}, x1 = {};
+                if (qv) {
+                    x0 = *reinterpret_cast<const f4*>(qrow + 32 * cc + 8 * g);
+                    x1 = *reinterpret_cast<const f4*>(qrow + 32 * cc + 8 * g + 4);
                 }
-                x *= f;
-                const bool ok = bid >= 0 && pos0 + 4 * g + r < end;
-                s[j][r] = ok ? x : -__builtin_inff();
-                mx = fmaxf(mx, s[j][r]);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float x = i < 4 ? x0[i] : x1[i - 4];
+                    const _Float16 hi = (_Float16)x;
+                    qa[cc][i] = c < 8 ? hi : (_Float16)(x - (float)hi);
+                }
+            }
+            if constexpr (Dims<D>::REM) {
+                f4 x = {};
+                if (qv) x = *reinterpret_cast<const f4*>(qrow + 32 * NC32 + 4 * g);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const _Float16 hi = (_Float16)x[i];
+                    qr[i] = c < 8 ? hi : (_Float16)(x[i] - (float)hi);
+                }
             }
         }
-        mx = fmaxf(mx, shfl_xor(mx, 16));
-        mx = fmaxf(mx, shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = fast_exp2(m_run - m_new);
-        m_run = m_new;
-        if (__any(alpha != 1.0f)) {
-            // Accumulator row 4g + r belongs to head (4g + r) & 7.
+
+        f4 o[NT];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float a = shfl(alpha, (4 * g + r) & 7);
-#pragma unroll
-                for (int t = 0; t < NT; ++t) o[t][r] *= a;
+        for (int t = 0; t < NT; ++t) o[t] = f4{0.f, 0.f, 0.f, 0.f};
+        float m_run = kMaxSeed, l_run = 0.f;
+
+        for (int ch = t0; ch < t1; ch += 64) {
+            const int ntiles = min(64, t1 - ch);
+            // Physical block of tile ch + j in lane j (-1: past the table or
+            // an id outside the pool).
+            int my_bid = -1, my_off = 0;
+            if (lane < ntiles) {
+                const int pos = (ch + lane) * kTile;
+                const int lb = pos / p.block_size;
+                my_off = pos - lb * p.block_size;
+                if (lb < tlen) {
+                    const int id = p.block_tables[(int64_t)s * p.max_blocks + lb];
+                    if (id >= 0 && (int64_t)id < p.num_blocks) my_bid = id;
+                }
             }
-        }
-        float lsum = 0.f;
+
+            auto load_step = [&](Tile<KV, D>(&buf)[kTilesPerIter], int it) {
 #pragma unroll
-        for (int j = 0; j < kTilesPerIter; ++j) {
-            h4 pa;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float pr = fast_exp2(s[j][r] - m_new);
-                lsum += pr;
-                if constexpr (KV == VCPP_KV_I8) {
-                    const uint32_t w = (uint32_t)(r < 2 ? cur[j].vs.x : cur[j].vs.y);
-                    float sv = h_to_f((r & 1) ? (w >> 16) : (w & 0xFFFFu));
+                for (int j = 0; j < kTilesPerIter; ++j) {
                     const int tt = it * kTilesPerIter + j;
-                    const bool ok = start + tt * kTile + 4 * g + r < end;
-                    pr *= ok ? sv : 0.f;
+                    const int bid = tt < ntiles ? __builtin_amdgcn_readlane(my_bid, tt & 63) : -1;
+                    const int off = __builtin_amdgcn_readlane(my_off, tt & 63);
+                    load_tile<KV, D>(buf[j], p, bid, off, lofs);
                 }
-                const _Float16 hi = (_Float16)pr;
-                pa[r] = c < 8 ? hi : (_Float16)(pr - (float)hi);
-            }
-            const _Float16* vt = lds + j * kTile * VROW;
+            };
+
+            auto compute_step = [&](const Tile<KV, D>(&cur)[kTilesPerIter], int it) {
+                float sc[kTilesPerIter][4];
+                float mx = kMaxSeed;
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                h4 vb;
+                for (int j = 0; j < kTilesPerIter; ++j) {
+                    const int tt = it * kTilesPerIter + j;
+                    const int bid = tt < ntiles ? __builtin_amdgcn_readlane(my_bid, tt & 63) : -1;
+                    const int pos0 = (ch + tt) * kTile;
+                    const bool full = bid >= 0 && pos0 + kTile <= end;  // wave-uniform
+                    f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int r = 0; r < 4; ++r) vb[r] = vt[(4 * g + r) * VROW + 16 * t + c];
-                o[t] = mfma16(pa, vb, o[t]);
+                    for (int cc = 0; cc < NC32; ++cc)
+                        acc = mfma32(k_chunk<KV, D>(cur[j], cc), qa[cc], acc);
+                    if constexpr (Dims<D>::REM) {
+                        // Own accumulator, summed on the VALU (see Dims).
+                        const f4 zero = {0.f, 0.f, 0.f, 0.f};
+                        const f4 acc2 = mfma16(k_rem<KV, D>(cur[j]), qr, zero);
+                        acc += acc2;
+                    }
+                    stage_v<KV, D>(lds + j * kTile * D * 2, cur[j], full || pos0 + c < end, g, c);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        float x = acc[r] + dpp_ror8(acc[r]);
+                        float f = p.scale_log2;
+                        if constexpr (KV == VCPP_KV_I8) {
+                            const uint32_t wd = (uint32_t)(r < 2 ? cur[j].ks.x : cur[j].ks.y);
+                            f *= h_to_f((r & 1) ? (wd >> 16) : (wd & 0xFFFFu));
+                        }
+                        x *= f;
+                        if (!full) x = (bid >= 0 && pos0 + 4 * g + r < end) ? x : -__builtin_inff();
+                        sc[j][r] = x;
+                        mx = fmaxf(mx, x);
+                    }
+                }
+                mx = fmaxf(mx, shfl_xor(mx, 16));
+                mx = fmaxf(mx, shfl_xor(mx, 32));
+                const float m_new = fmaxf(m_run, mx);
+                const float alpha = fast_exp2(m_run - m_new);
+                m_run = m_new;
+                if (__any(alpha != 1.0f)) {
+                    // Accumulator row 4g + r belongs to head (4g + r) & 7.
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float al = shfl(alpha, (4 * g + r) & 7);
+#pragma unroll
+                        for (int t = 0; t < NT; ++t) o[t][r] *= al;
+                    }
+                }
+                float lsum = 0.f;
+#pragma unroll
+                for (int j = 0; j < kTilesPerIter; ++j) {
+                    h4 pa;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        float pr = fast_exp2(sc[j][r] - m_new);
+                        lsum += pr;
+                        if constexpr (KV == VCPP_KV_I8) {
+                            const uint32_t wd = (uint32_t)(r < 2 ? cur[j].vs.x : cur[j].vs.y);
+                            // masked tokens have pr == 0; the select keeps 0 * garbage out
+                            pr = pr > 0.f ? pr * h_to_f((r & 1) ? (wd >> 16) : (wd & 0xFFFFu)) : 0.f;
+                        }
+                        const _Float16 hi = (_Float16)pr;
+                        pa[r] = c < 8 ? hi : (_Float16)(pr - (float)hi);
+                    }
+                    lds_char* vt = lds + j * kTile * D * 2;
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) o[t] = mfma16(pa, read_v_tr<D>(vt, t, g, c), o[t]);
+                }
+                l_run = l_run * alpha + lsum;
+            };
+
+            // Two register buffers in ping-pong: step it+1 is in flight while
+            // step it computes; no buffer is copied (a copy would wait on its
+            // loads).  Steps past the end load zero-sized (free) tiles.
+            Tile<KV, D> buf_a[kTilesPerIter], buf_b[kTilesPerIter];
+            const int niters = (ntiles + kTilesPerIter - 1) / kTilesPerIter;
+            load_step(buf_a, 0);
+            for (int it = 0; it < niters; it += 2) {
+                load_step(buf_b, it + 1);
+                compute_step(buf_a, it);
+                if (it + 1 >= niters) break;
+                load_step(buf_a, it + 2);
+                compute_step(buf_b, it + 1);
             }
         }
-        l_run = l_run * alpha + lsum;
 
-        if (it + 1 < niters) {
+        // Per-head totals: l over the four lane groups; O rows h (hi) + h + 8 (lo).
+        float lt = l_run;
+        lt += shfl_xor(lt, 16);
+        lt += shfl_xor(lt, 32);
 #pragma unroll
-            for (int j = 0; j < kTilesPerIter; ++j) cur[j] = nxt[j];
-        }
-    }
-
-    // Per-head totals: l over the four lane groups; O rows h (hi) + h + 8 (lo).
-    l_run += shfl_xor(l_run, 16);
-    l_run += shfl_xor(l_run, 32);
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o[t][r] += shfl_xor(o[t][r], 32);
-
-    float lh[4], mh[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        lh[r] = shfl(l_run, (4 * g + r) & 7);
-        mh[r] = shfl(m_run, (4 * g + r) & 7);
-    }
-    if (g >= 2) return;
-    if (np == 1) {
+            for (int r = 0; r < 4; ++r) o[t][r] += shfl_xor(o[t][r], 32);
+        float lh[4], mh[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int h = 4 * g + r;
-            if (h >= gc) continue;
-            const float inv = 1.0f / (lh[r] + 1e-9f);
-            float* orow = p.out + ((int64_t)seq * p.num_heads + head_base + h) * D;
-#pragma unroll
-            for (int t = 0; t < NT; ++t) orow[16 * t + c] = o[t][r] * inv;
+            lh[r] = shfl(lt, (4 * g + r) & 7);
+            mh[r] = shfl(m_run, (4 * g + r) & 7);
         }
-    } else {
+        if (g < 2) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int h = 4 * g + r;
-            if (h >= gc) continue;
-            const int64_t idx = ((int64_t)seq * p.max_parts + part) * p.num_heads + head_base + h;
-            float* orow = p.ws_o + idx * D;
+            for (int r = 0; r < 4; ++r) {
+                const int h = 4 * g + r;
+                if (h >= gc) continue;
+                const int head = head_base + h;
+                if (complete) {
+                    const float inv = 1.0f / (lh[r] + 1e-9f);
+                    float* orow = p.out + ((int64_t)s * p.num_heads + head) * D;
 #pragma unroll
-            for (int t = 0; t < NT; ++t) orow[16 * t + c] = o[t][r];
-            if (c == 0) p.ws_ml[idx] = make_float2(mh[r], lh[r]);
+                    for (int t = 0; t < NT; ++t) orow[16 * t + c] = o[t][r] * inv;
+                } else {
+                    const int64_t idx = ((int64_t)w * 2 + slot) * p.num_heads + head;
+                    float* orow = p.ws_o + idx * D;
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) orow[16 * t + c] = o[t][r];
+                    if (c == 0) p.ws_ml[idx] = make_float2(mh[r], lh[r]);
+                }
+            }
         }
     }
 }
 
-// fp32 pages: plain VALU kernel, one wave per (partition, sequence, head).
-// Logits of the partition live in LDS; same partial format as the MFMA path.
+// Log-sum-exp merge of the fragments of one (sequence, head) per wave, and
+// zeros for sequences without tiles.  Fragment order: the first range holds
+// the sequence in slot 1, every later range in slot 0.
+__global__ __launch_bounds__(256) void merge_split_kernel(DecodeParams p) {
+    const int lane = threadIdx.x & 63;
+    const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
+    const int s = blockIdx.x;
+    if (head >= p.num_heads) return;
+    const int D = p.head_dim;
+    float* out = p.out + ((int64_t)s * p.num_heads + head) * D;
+    const int S = p.tile_start[s], E = p.tile_start[s + 1], T = p.tile_start[p.num_seqs];
+    if (E <= S) {
+        for (int d = lane; d < D; d += 64) out[d] = 0.f;
+        return;
+    }
+    const int G = p.num_wg;
+    // range holding tile t: the largest w with floor(w T / G) <= t
+    const int w0 = (int)(((int64_t)(S + 1) * G - 1) / T);
+    const int w1 = (int)(((int64_t)E * G - 1) / T);
+    if (w0 == w1) return;  // finished in place
+    const int nf = w1 - w0 + 1;
+    auto frag = [&](int i) -> int64_t {
+        return ((int64_t)(w0 + i) * 2 + (i == 0 ? 1 : 0)) * p.num_heads + head;
+    };
+    // A range can be empty when there are fewer tiles than ranges; it wrote
+    // nothing, so its slot holds stale data and must not take part.
+    auto live = [&](int i) -> bool {
+        return i < nf && range_start(w0 + i, T, G) < range_start(w0 + i + 1, T, G);
+    };
+    float M = kMaxSeed, L = 0.f;
+    for (int i0 = 0; i0 < nf; i0 += 64) {
+        const int i = i0 + lane;
+        float2 ml = make_float2(kMaxSeed, 0.f);
+        if (live(i)) ml = p.ws_ml[frag(i)];
+        float m = ml.x;
+        for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));
+        const float Mn = fmaxf(M, m);
+        float l = fast_exp2(ml.x - Mn) * ml.y;
+        for (int k = 32; k >= 1; k >>= 1) l += shfl_xor(l, k);
+        L = L * fast_exp2(M - Mn) + l;
+        M = Mn;
+    }
+    const float inv = 1.0f / (L + 1e-9f);
+    // Weights are broadcast with readlane (EXEC-independent); the d loop may
+    // leave lanes inactive when head_dim is not a multiple of 64.
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // d = lane + 64 k, head_dim <= 256
+    for (int i0 = 0; i0 < nf; i0 += 64) {
+        const int n = min(64, nf - i0);
+        float wt = 0.f;
+        if (live(i0 + lane)) wt = fast_exp2(p.ws_ml[frag(i0 + lane)].x - M);
+        for (int j = 0; j < n; ++j) {
+            const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wt), j));
+            if (wj == 0.f) continue;  // empty range or negligible weight (uniform)
+            const float* orow = p.ws_o + frag(i0 + j) * D;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (lane + 64 * k < D) acc[k] += wj * orow[lane + 64 * k];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (lane + 64 * k < D) out[lane + 64 * k] = acc[k] * inv;
+}
+
+// ---- fp32 pages -----------------------------------------------------------
+
+// Plain VALU kernel, one wave per (partition, sequence, head).  Logits of the
+// partition live in LDS; the exp2/log2-scaled partials match the merge below.
 __global__ __launch_bounds__(64) void decode_f32_kernel(DecodeParams p) {
     __shared__ float sl[1024];
     extern __shared__ float qs_dyn[];
@@ -438,14 +606,14 @@ __global__ __launch_bounds__(64) void decode_f32_kernel(DecodeParams p) {
     for (int d = lane; d < D; d += 64) {
         float acc = 0.f;
         for (int i = 0; i < n; ++i) {
-            const float w = sl[i];
-            if (w == 0.f) continue;
+            const float wt = sl[i];
+            if (wt == 0.f) continue;
             const int pos = start + i;
             const int lb = pos / p.block_size;
             const int id = p.block_tables[(int64_t)seq * p.max_blocks + lb];
             const float* vr = vb + (int64_t)id * p.block_stride +
                               ((int64_t)(pos - lb * p.block_size) * p.num_kv_heads + kvh) * D;
-            acc = fmaf(w, vr[d], acc);
+            acc = fmaf(wt, vr[d], acc);
         }
         if (np == 1) {
             p.out[((int64_t)seq * p.num_heads + head) * D + d] = acc / (l + 1e-9f);
@@ -457,8 +625,8 @@ __global__ __launch_bounds__(64) void decode_f32_kernel(DecodeParams p) {
     }
 }
 
-// Log-sum-exp merge of the partitions of one (sequence, head) per wave.
-__global__ __launch_bounds__(256) void lse_merge_kernel(DecodeParams p) {
+// Log-sum-exp merge of the fixed partitions of one (sequence, head) per wave.
+__global__ __launch_bounds__(256) void merge_parts_kernel(DecodeParams p) {
     const int lane = threadIdx.x & 63;
     const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
     const int seq = blockIdx.x;
@@ -469,44 +637,80 @@ __global__ __launch_bounds__(256) void lse_merge_kernel(DecodeParams p) {
     if (np <= 1) return;
     const int D = p.head_dim;
     const int64_t base = (int64_t)seq * p.max_parts * p.num_heads + head;
-    float M = kMaxSeed;
-    for (int i = 0; i < np; ++i) M = fmaxf(M, p.ws_ml[base + (int64_t)i * p.num_heads].x);
-    float L = 0.f;
-    for (int i = 0; i < np; ++i) {
-        const float2 ml = p.ws_ml[base + (int64_t)i * p.num_heads];
-        L += fast_exp2(ml.x - M) * ml.y;
+    float M = kMaxSeed, L = 0.f;
+    for (int i0 = 0; i0 < np; i0 += 64) {
+        const int i = i0 + lane;
+        float2 ml = make_float2(kMaxSeed, 0.f);
+        if (i < np) ml = p.ws_ml[base + (int64_t)i * p.num_heads];
+        float m = ml.x;
+        for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));
+        const float Mn = fmaxf(M, m);
+        float l = fast_exp2(ml.x - Mn) * ml.y;
+        for (int k = 32; k >= 1; k >>= 1) l += shfl_xor(l, k);
+        L = L * fast_exp2(M - Mn) + l;
+        M = Mn;
     }
     const float inv = 1.0f / (L + 1e-9f);
-    for (int d = lane; d < D; d += 64) {
-        float acc = 0.f;
-        for (int i = 0; i < np; ++i) {
-            const int64_t idx = base + (int64_t)i * p.num_heads;
-            acc += fast_exp2(p.ws_ml[idx].x - M) * p.ws_o[idx * D + d];
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int i0 = 0; i0 < np; i0 += 64) {
+        const int n = min(64, np - i0);
+        float wt = 0.f;
+        if (i0 + lane < np) wt = fast_exp2(p.ws_ml[base + (int64_t)(i0 + lane) * p.num_heads].x - M);
+        for (int j = 0; j < n; ++j) {
+            const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wt), j));
+            const float* orow = p.ws_o + (base + (int64_t)(i0 + j) * p.num_heads) * D;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (lane + 64 * k < D) acc[k] += wj * orow[lane + 64 * k];
         }
-        p.out[((int64_t)seq * p.num_heads + head) * D + d] = acc * inv;
     }
+    float* out = p.out + ((int64_t)seq * p.num_heads + head) * D;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (lane + 64 * k < D) out[lane + 64 * k] = acc[k] * inv;
 }
 
 template <int KV, int D>
 hipError_t launch_mfma(const DecodeParams& p, hipStream_t stream) {
-    const int wpw = p.pairs < 8 ? p.pairs : 8;
-    dim3 grid(p.max_parts, p.num_seqs, (p.pairs + wpw - 1) / wpw);
-    const size_t lds = (size_t)wpw * kTilesPerIter * kTile * Dims<D>::VROW * sizeof(_Float16);
+    const int wpw = p.pairs < kWavesPerGroup ? p.pairs : kWavesPerGroup;
+    dim3 grid(p.num_wg, (p.pairs + wpw - 1) / wpw);
+    const size_t lds = (size_t)wpw * kTilesPerIter * kTile * D * sizeof(_Float16);
     hipLaunchKernelGGL((decode_mfma_kernel<KV, D>), grid, dim3(wpw * 64), lds, stream, p);
     return hipGetLastError();
 }
 
 }  // namespace
 
+int decode_group_count(int pairs) {
+    const int wpw = pairs < kWavesPerGroup ? pairs : kWavesPerGroup;
+    return (pairs + wpw - 1) / wpw;
+}
+
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
     if (p.num_seqs == 0) return hipSuccess;
     hipError_t err;
+    const bool prof = prof_enabled();
     if (p.kv_dtype == VCPP_KV_F32) {
+        if (prof) prof_begin(kKernelDecode, stream);
         dim3 grid(p.max_parts, p.num_seqs, p.num_heads);
         hipLaunchKernelGGL(decode_f32_kernel, grid, dim3(64), p.head_dim * sizeof(float), stream,
                            p);
         err = hipGetLastError();
-    } else {
+        if (err != hipSuccess) return err;
+        if (prof) prof_end(kKernelDecode, stream);
+        if (p.max_parts > 1) {
+            if (prof) prof_begin(kKernelMerge, stream);
+            dim3 mg(p.num_seqs, (p.num_heads + 3) / 4);
+            hipLaunchKernelGGL(merge_parts_kernel, mg, dim3(256), 0, stream, p);
+            err = hipGetLastError();
+            if (prof) prof_end(kKernelMerge, stream);
+        }
+        return err;
+    }
+    hipLaunchKernelGGL(split_scan_kernel, dim3(1), dim3(1024), 0, stream, p);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    if (prof) prof_begin(kKernelDecode, stream);
 #define VCPP_DISPATCH_D(KVT)                                              \
     switch (p.head_dim) {                                                 \
         case 64: err = launch_mfma<KVT, 64>(p, stream); break;            \
@@ -514,24 +718,24 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
         case 128: err = launch_mfma<KVT, 128>(p, stream); break;          \
         default: return hipErrorInvalidValue;                             \
     }
-        if (p.kv_dtype == VCPP_KV_F16) {
-            VCPP_DISPATCH_D(VCPP_KV_F16)
-        } else {
-            VCPP_DISPATCH_D(VCPP_KV_I8)
-        }
+    if (p.kv_dtype == VCPP_KV_F16) {
+        VCPP_DISPATCH_D(VCPP_KV_F16)
+    } else {
+        VCPP_DISPATCH_D(VCPP_KV_I8)
+    }
 #undef VCPP_DISPATCH_D
-    }
     if (err != hipSuccess) return err;
-    if (p.max_parts > 1) {
-        dim3 grid(p.num_seqs, (p.num_heads + 3) / 4);
-        hipLaunchKernelGGL(lse_merge_kernel, grid, dim3(256), 0, stream, p);
-        err = hipGetLastError();
-    }
+    if (prof) prof_end(kKernelDecode, stream);
+    if (prof) prof_begin(kKernelMerge, stream);
+    dim3 mg(p.num_seqs, (p.num_heads + 3) / 4);
+    hipLaunchKernelGGL(merge_split_kernel, mg, dim3(256), 0, stream, p);
+    err = hipGetLastError();
+    if (prof) prof_end(kKernelMerge, stream);
     return err;
 }
 
 bool decode_head_dim_supported(int kv_dtype, int head_dim) {
-    if (kv_dtype == VCPP_KV_F32) return head_dim > 0 && head_dim <= 1024 && head_dim % 4 == 0;
+    if (kv_dtype == VCPP_KV_F32) return head_dim > 0 && head_dim <= 256 && head_dim % 4 == 0;
     return head_dim == 64 || head_dim == 80 || head_dim == 128;
 }
 

@@ -27,9 +27,12 @@ EXPORTS = [
     "vcpp_version",
     "vcpp_paged_decode",
     "vcpp_decode_workspace_size",
-    "vcpp_decode_default_partition",
     "paged_attention_cuda",
+    "vcpp_profile_enable",
+    "vcpp_profile_read",
 ]
+
+KERNEL_DECODE, KERNEL_MERGE, KERNEL_PREFILL = 0, 1, 2
 
 
 class KVPages(ctypes.Structure):
@@ -72,12 +75,15 @@ def lib():
     L.vcpp_paged_decode.argtypes = [ctypes.POINTER(KVPages), vp, vp, vp, i32, vp, vp, i32, i32,
                                     i32, i32, vp, sz, vp]
     L.vcpp_paged_decode.restype = ctypes.c_int
-    L.vcpp_decode_workspace_size.argtypes = [i32, i32, i32, i32, i32]
+    L.vcpp_decode_workspace_size.argtypes = [ctypes.POINTER(KVPages), i32, i32, i32, i32]
     L.vcpp_decode_workspace_size.restype = sz
-    L.vcpp_decode_default_partition.argtypes = [i32, i32, i32]
-    L.vcpp_decode_default_partition.restype = i32
     L.paged_attention_cuda.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32]
     L.paged_attention_cuda.restype = None
+    L.vcpp_profile_enable.argtypes = [ctypes.c_int]
+    L.vcpp_profile_enable.restype = ctypes.c_int
+    L.vcpp_profile_read.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                    ctypes.POINTER(ctypes.c_int64)]
+    L.vcpp_profile_read.restype = ctypes.c_int
     _lib = L
     return L
 
@@ -111,9 +117,9 @@ def kv_pages(dtype, k, v, block_size, num_kv_heads, head_dim, num_blocks, block_
                    None if v_scale is None else v_scale.data_ptr())
 
 
-def decode_workspace_size(num_seqs, num_heads, head_dim, max_context_len, partition_size=0):
-    return lib().vcpp_decode_workspace_size(num_seqs, num_heads, head_dim, max_context_len,
-                                            partition_size)
+def decode_workspace_size(pages, num_seqs, num_heads, max_context_len, partition_size=0):
+    return lib().vcpp_decode_workspace_size(ctypes.byref(pages), num_seqs, num_heads,
+                                            max_context_len, partition_size)
 
 
 def paged_decode(pages, q, out, block_tables, context_lens, max_context_len, num_heads,
@@ -122,8 +128,7 @@ def paged_decode(pages, q, out, block_tables, context_lens, max_context_len, num
     of at least decode_workspace_size(...) bytes (allocated here when None)."""
     num_seqs = q.shape[0]
     max_blocks = block_tables.shape[1] if block_tables is not None and block_tables.dim() == 2 else 0
-    need = decode_workspace_size(num_seqs, num_heads, pages.head_dim, max_context_len,
-                                 partition_size)
+    need = decode_workspace_size(pages, num_seqs, num_heads, max_context_len, partition_size)
     if workspace is None and need > 0:
         import torch
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
@@ -134,3 +139,15 @@ def paged_decode(pages, q, out, block_tables, context_lens, max_context_len, num
                                  ws_bytes, _stream(stream))
     _check(rc)
     return out
+
+
+def profile_enable(on=True):
+    _check(lib().vcpp_profile_enable(1 if on else 0))
+
+
+def profile_read(kernel_id):
+    """(total_ms, launches) of one kernel since the last profile_enable()."""
+    ms = ctypes.c_double()
+    n = ctypes.c_int64()
+    _check(lib().vcpp_profile_read(kernel_id, ctypes.byref(ms), ctypes.byref(n)))
+    return ms.value, n.value
