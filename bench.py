@@ -154,7 +154,7 @@ def main():
     pages0 = pyvcpp.kv_pages(pyvcpp.KV_F16, w["sets"][0][0], w["sets"][0][1], BS, HKV, D, w["nb"],
                              BS * HKV * D)
     need = pyvcpp.decode_workspace_size(pages0, 64, H, w["max_ctx"], args.partition)
-    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda:0")
+    ws = torch.zeros(max(need, 1), dtype=torch.uint8, device="cuda:0")
 
     run_decode_steps(torch, pyvcpp, w, args.warmup, ws, args.partition)
     torch.cuda.synchronize()

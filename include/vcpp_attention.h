@@ -101,7 +101,8 @@ typedef struct vcpp_kv_pages {
  *                partition -- a tuning and test knob.  Ranges that end inside a
  *                sequence leave partials, merged by a log-sum-exp kernel.
  *   workspace    device scratch of at least vcpp_decode_workspace_size(...)
- *                bytes (may be NULL when that size is 0).  Overwritten.
+ *                bytes (may be NULL when that size is 0); scratch for the
+ *                call only, so calls that may overlap need separate ones.
  * Replaces the per-request loop around paged_attention()
  * (src/paged_engine.cpp:505-508, src/paged_attention.cpp:96-121).
  */

@@ -152,3 +152,27 @@ def test_v1_entry(cuda):
     torch.cuda.synchronize()
     assert pyvcpp.last_error() == ""
     assert_close(out.cpu().numpy(), want, *TOL[O.ORC_F16], what="v1")
+
+
+@pytest.mark.parametrize("partition", [0, 32, 128])
+def test_workspace_reuse(cuda, partition):
+    """One zero-initialised workspace across many calls with changing q and
+    pages: the fragment arrival counters must return to zero after each call
+    and no call may see a previous call's partials."""
+    nb = 400
+    pools = [O.make_pool(O.ORC_F16, 300 + i, nb, 8, 80) for i in range(2)]
+    dpools = [DevPool(pl) for pl in pools]
+    ctx = np.array([1500, 40, 777, 16, 2900, 0, 129, 700], dtype=np.int32)
+    tables = random_tables(311, ctx, nb)
+    td, cd = dev(tables), dev(ctx)
+    need = pyvcpp.decode_workspace_size(dpools[0].pages, len(ctx), 64, int(ctx.max()), partition)
+    ws = torch.zeros(max(need, 1), dtype=torch.uint8, device="cuda:0")
+    for it in range(6):
+        q = O.normal(400 + it, (len(ctx), 64, 80))
+        want = O.decode(pools[it % 2], q, tables, ctx, 64)
+        qd = dev(q)
+        out = torch.full_like(qd, float("nan"))
+        pyvcpp.paged_decode(dpools[it % 2].pages, qd, out, td, cd, int(ctx.max()), 64,
+                            partition_size=partition, workspace=ws)
+        torch.cuda.synchronize()
+        assert_close(out.cpu().numpy(), want, *TOL[O.ORC_F16], what="reuse it=%d" % it)

@@ -10,6 +10,7 @@
 #include <cstdarg>
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -69,7 +70,7 @@ struct DecodePlan {
     int32_t num_wg = 0;      // fp16/int8: workgroup ranges per kv-head group
     int32_t partition = 0;   // fp32: tokens per partition
     int32_t max_parts = 0;   // fp32: partitions per sequence
-    size_t off_tile_start = 0, off_first_seq = 0, off_o = 0, off_ml = 0, bytes = 0;
+    size_t off_o = 0, off_ml = 0, bytes = 0;
 };
 
 DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_heads,
@@ -102,12 +103,10 @@ DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_he
     }
     G = std::max<int64_t>(1, std::min<int64_t>(G, kMaxRanges));
     pl.num_wg = (int32_t)G;
-    pl.off_tile_start = 0;
-    pl.off_first_seq = align256(sizeof(int32_t) * ((size_t)num_seqs + 1));
-    pl.off_o = pl.off_first_seq + align256(sizeof(int32_t) * (size_t)G);
-    const size_t rows = (size_t)G * 2 * num_heads;
-    pl.off_ml = pl.off_o + align256(rows * D * sizeof(float));
-    pl.bytes = pl.off_ml + align256(rows * sizeof(float2));
+    pl.off_o = 0;
+    const size_t blocks = (size_t)G * 2 * pairs;  // [range][slot][kv-head slot]
+    pl.off_ml = pl.off_o + align256(blocks * 8 * D * sizeof(float));
+    pl.bytes = pl.off_ml + align256(blocks * 16 * sizeof(float2));
     return pl;
 }
 
@@ -238,10 +237,12 @@ int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
     p.num_wg = pl.num_wg;
     p.ctx_cap = max_context_len;
     if (need > 0) {
-        p.tile_start = reinterpret_cast<int32_t*>(ws + pl.off_tile_start);
-        p.first_seq = reinterpret_cast<int32_t*>(ws + pl.off_first_seq);
         p.ws_o = reinterpret_cast<float*>(ws + pl.off_o);
         p.ws_ml = reinterpret_cast<float2*>(ws + pl.off_ml);
+    }
+    {
+        const char* e = getenv("VCPP_DECODE_PIPELINE");
+        p.pipeline = e ? atoi(e) : 0;
     }
     p.scale_log2 = (1.0f / std::sqrt((float)kv->head_dim)) * 1.4426950408889634f;
     if (p.pairs > 65535 * 8) return fail(VCPP_E_UNSUPPORTED, "too many kv heads");

@@ -39,15 +39,15 @@ struct DecodeParams {
     // num_wg workgroup ranges (per kv-head group)
     int32_t num_wg;
     int32_t ctx_cap;       // context lengths are clamped to this
-    int32_t* tile_start;   // [num_seqs + 1] exclusive prefix of tiles per sequence
-    int32_t* first_seq;    // [num_wg] sequence holding each range's first tile
     // fp32: fixed partitions of `partition` tokens, max_parts per sequence
     int32_t partition;
     int32_t max_parts;
-    // partials: fp16/int8 [num_wg][2 slots][num_heads], fp32 [num_seqs][max_parts][num_heads]
+    // partials: fp16/int8 blocks [num_wg][2 slots][pairs] of [8 heads][head_dim] outputs and
+    // 16 (m, l) pairs; fp32 [num_seqs][max_parts][num_heads]
     float* ws_o;     // (.., head_dim) unnormalised outputs
     float2* ws_ml;   // (max in log2 units, sum of exponentials)
     float scale_log2;  // log2(e) / sqrt(head_dim)
+    int32_t pipeline;  // fp16/int8 pipeline shape (tuning; 0 = default)
 };
 
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);

@@ -39,12 +39,16 @@
 #include "device_common.h"
 #include "profile.h"
 
+#include <cstdlib>
+#include <type_traits>
+
 namespace vcpp {
 
 namespace {
 
 constexpr int kTile = 16;          // tokens per MFMA tile
-constexpr int kTilesPerIter = 4;   // tiles per softmax update / prefetch step
+// Pipeline shape (template parameters of the kernel): TPS tiles per step
+// (one softmax update), NBUF register buffers, loads issued NBUF-1 steps ahead.
 // Waves (kv heads) per workgroup: 4 kv heads x 80 dims x 2 B = 640 B, five
 // whole 128-byte lines of every token row.
 constexpr int kWavesPerGroup = 4;
@@ -218,51 +222,124 @@ __device__ __forceinline__ int range_start(int w, int T, int G) {
     return (int)(((int64_t)w * T) / G);
 }
 
-// ---- scan: tile prefix sums and each workgroup's first sequence -----------
-
-__global__ __launch_bounds__(1024) void split_scan_kernel(DecodeParams p) {
-    __shared__ int wave_sums[16];
-    __shared__ int carry_s;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid == 0) carry_s = 0;
-    __syncthreads();
-    for (int base = 0; base < p.num_seqs; base += 1024) {
-        const int s = base + tid;
-        const int nt = s < p.num_seqs ? tiles_of(p, s) : 0;
-        int x = nt;
+// Sum over the wave's lanes, returned as a scalar (provably uniform).
+__device__ __forceinline__ int wave_sum(int x) {
 #pragma unroll
-        for (int k = 1; k < 64; k <<= 1) {
-            const int y = __shfl_up(x, k, 64);
-            if (lane >= k) x += y;
-        }
-        if (lane == 63) wave_sums[wave] = x;
-        __syncthreads();
-        int before = carry_s;
-        for (int w2 = 0; w2 < wave; ++w2) before += wave_sums[w2];
-        if (s < p.num_seqs) p.tile_start[s] = before + x - nt;
-        __syncthreads();
-        if (tid == 1023) carry_s = before + x;
-        __syncthreads();
+    for (int k = 32; k >= 1; k >>= 1) x += __shfl_xor(x, k, 64);
+    return __builtin_amdgcn_readfirstlane(x);
+}
+
+// Exclusive prefix sum over the wave's lanes.
+__device__ __forceinline__ int wave_excl_scan(int x, int lane) {
+    int y = x;
+#pragma unroll
+    for (int k = 1; k < 64; k <<= 1) {
+        const int t = __shfl_up(y, k, 64);
+        if (lane >= k) y += t;
     }
-    const int T = carry_s;
-    if (tid == 0) p.tile_start[p.num_seqs] = T;
-    __syncthreads();
-    // first_seq[w] = the sequence holding tile range_start(w) (num_seqs if none).
-    for (int w = tid; w < p.num_wg; w += 1024) {
-        const int a = range_start(w, T, p.num_wg);
-        int lo = 0, hi = p.num_seqs;  // smallest s with tile_start[s + 1] > a
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if (p.tile_start[mid + 1] > a) hi = mid;
-            else lo = mid + 1;
+    return y - x;
+}
+
+// Range holding tile t (0 <= t < T): the largest w with floor(w T / G) <= t.
+__device__ __forceinline__ int range_of(int t, int T, int G) {
+    return (int)(((int64_t)(t + 1) * G - 1) / T);
+}
+
+__device__ __forceinline__ bool range_live(int w, int T, int G) {
+    return T >= G || range_start(w, T, G) < range_start(w + 1, T, G);
+}
+
+// Partial block of fragment i (range w0 + i) of a sequence for kv-head slot
+// `pair`: the first range holds the sequence in slot 1 (it starts inside it),
+// every later one in slot 0.  Blocks are [8 heads][head_dim] floats for the
+// outputs (32 * head_dim bytes, whole 128-byte lines as head_dim % 16 == 0)
+// and 16 (m, l) pairs (128 bytes) for the softmax state, so no cache line is
+// shared by two blocks.
+__device__ __forceinline__ int64_t frag_block(int w0, int i, int pairs, int pair) {
+    return ((int64_t)(w0 + i) * 2 + (i == 0 ? 1 : 0)) * pairs + pair;
+}
+
+// Log-sum-exp merge of the fragments (ranges w0..w1) of sequence s for one
+// wave's heads head_base .. head_base+gc-1.  Each chunk of 8 fragments is one
+// round of loads: every (m, l) and every partial output of the chunk is
+// requested before any is used, then folded in with an online rescale.
+// Lane (i8, h) = (lane / 8, lane % 8) owns fragment weights; output element
+// e = lane + 64 k (head e / D) of the 8 x D block is lane-owned.  `wts` is the
+// wave's LDS scratch (>= 80 floats).
+template <int D>
+__device__ __forceinline__ void merge_fragments(const DecodeParams& p, int s, int w0, int w1,
+                                                int pair, int head_base, int gc, int T, int lane,
+                                                __attribute__((address_space(3))) float* wts) {
+    // output element e = 4 lane + 256 k4 (.. +3, all in head e / D since D % 4 == 0)
+    constexpr int K4 = (8 * D + 255) / 256;
+    const int G = p.num_wg;
+    const int nfr = w1 - w0 + 1;
+    const int i8 = lane >> 3, h = lane & 7;
+    const int n_out = gc * D;
+    const auto mlr = make_rsrc(p.ws_ml, 0x7FFFFFFF);
+    float M = kMaxSeed, L = 0.f;  // of head h
+    f4 acc[K4];
+#pragma unroll
+    for (int k = 0; k < K4; ++k) acc[k] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int i0 = 0; i0 < nfr; i0 += 8) {
+        // one round of loads for the chunk
+        float2 ml = make_float2(kMaxSeed, 0.f);
+        {
+            const int i = i0 + i8;
+            const bool ok = i < nfr && h < gc && range_live(w0 + i, T, G);
+            const int64_t idx = frag_block(w0, ok ? i : 0, p.pairs, pair) * 16 + h;
+            const float2 x = __builtin_bit_cast(
+                float2, __builtin_amdgcn_raw_buffer_load_b64(mlr, (int)(idx * 8), 0, 0));
+            if (ok) ml = x;
         }
-        p.first_seq[w] = lo;
+        f4 v[8][K4];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            // an empty or missing fragment reads fragment 0 (weight 0 below)
+            const int i = i0 + j;
+            const bool ok = i < nfr && range_live(w0 + i, T, G);
+            const float* row = p.ws_o + frag_block(w0, ok ? i : 0, p.pairs, pair) * (8 * D);
+            const auto rr = make_rsrc(row, n_out * 4);
+#pragma unroll
+            for (int k = 0; k < K4; ++k)
+                v[j][k] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                     rr, (4 * lane + 256 * k) * 4, 0, 0));
+        }
+        // running max / sum of head h, chunk weights
+        float cm = ml.x;
+        cm = fmaxf(cm, __shfl_xor(cm, 8, 64));
+        cm = fmaxf(cm, __shfl_xor(cm, 16, 64));
+        cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
+        const float Mn = fmaxf(M, cm);
+        const float wt = fast_exp2(ml.x - Mn);  // 0 for empty fragments
+        float cl = wt * ml.y;
+        cl += __shfl_xor(cl, 8, 64);
+        cl += __shfl_xor(cl, 16, 64);
+        cl += __shfl_xor(cl, 32, 64);
+        const float resc = fast_exp2(M - Mn);
+        L = L * resc + cl;
+        M = Mn;
+        wts[lane] = wt;                       // wts[i8 * 8 + h]
+        if (lane < 8) wts[64 + lane] = resc;  // rescale of head `lane`
+#pragma unroll
+        for (int k = 0; k < K4; ++k) {
+            const int hk = min((4 * lane + 256 * k) / D, 7);
+            f4 a = acc[k] * wts[64 + hk];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) a += wts[j * 8 + hk] * v[j][k];
+            acc[k] = a;
+        }
+    }
+    if (lane < 8) wts[72 + lane] = 1.0f / (L + 1e-9f);
+    float* out = p.out + ((int64_t)s * p.num_heads + head_base) * D;
+#pragma unroll
+    for (int k = 0; k < K4; ++k) {
+        const int e = 4 * lane + 256 * k;
+        if (e < n_out) *reinterpret_cast<f4*>(out + e) = acc[k] * wts[72 + e / D];
     }
 }
 
-// ---- the decode kernel ----------------------------------------------------
-
-template <int KV, int D>
+template <int KV, int D, int TPS, int NBUF>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void decode_mfma_kernel(DecodeParams p) {
     constexpr int NC32 = Dims<D>::NC32, NT = Dims<D>::NT;
@@ -274,21 +351,25 @@ void decode_mfma_kernel(DecodeParams p) {
     const int pair = blockIdx.y * (blockDim.x >> 6) + wave;
     if (pair >= p.pairs) return;  // whole waves only; no workgroup barriers below
     const int w = blockIdx.x, G = p.num_wg;
-    const int T = p.tile_start[p.num_seqs];
-    const int a = range_start(w, T, G), b = range_start(w + 1, T, G);
-    if (a >= b) return;
 
     const int kvh = pair / p.qchunks, qc = pair - kvh * p.qchunks;
     const int head_base = kvh * p.group + qc * 8;
     const int gc = min(8, p.group - qc * 8);
     const LaneOffsets lofs = lane_offsets<KV, D>(p, kvh, g, c);
     lds_char* lds = reinterpret_cast<lds_char*>((__attribute__((address_space(3))) char*)lds_raw) +
-                    wave * (kTilesPerIter * kTile * D * 2);
+                    wave * (TPS * kTile * D * 2);
 
-    for (int s = p.first_seq[w]; s < p.num_seqs; ++s) {
-        const int S = p.tile_start[s], E = p.tile_start[s + 1];
-        if (S >= b) break;
-        if (E <= a) continue;  // zero-tile sequence before the range
+    // Tiles of all sequences laid end to end: total T, this workgroup's range
+    // [a, b) = [floor(w T / G), floor((w + 1) T / G)).
+    int T = 0;
+    for (int base = 0; base < p.num_seqs; base += 64)
+        T += wave_sum(base + lane < p.num_seqs ? tiles_of(p, base + lane) : 0);
+    const int a = range_start(w, T, G), b = range_start(w + 1, T, G);
+    // Zero-tile sequences are zeroed by the range their start falls into (the
+    // last range for those at T, range 0 when every sequence is empty).
+    const bool zero_owner_tail = (T == 0 && w == 0) || (T > 0 && w == G - 1);
+
+    auto process_fragment = [&](int s, int S, int E) {
         const int t0 = max(a, S) - S, t1 = min(b, E) - S;
         const bool complete = S >= a && E <= b;
         const int slot = S < a ? 0 : 1;
@@ -349,25 +430,28 @@ void decode_mfma_kernel(DecodeParams p) {
                 }
             }
 
-            auto load_step = [&](Tile<KV, D>(&buf)[kTilesPerIter], int it) {
+            auto load_step = [&](Tile<KV, D>(&buf)[TPS], int it) {
 #pragma unroll
-                for (int j = 0; j < kTilesPerIter; ++j) {
-                    const int tt = it * kTilesPerIter + j;
+                for (int j = 0; j < TPS; ++j) {
+                    const int tt = it * TPS + j;
                     const int bid = tt < ntiles ? __builtin_amdgcn_readlane(my_bid, tt & 63) : -1;
                     const int off = __builtin_amdgcn_readlane(my_off, tt & 63);
                     load_tile<KV, D>(buf[j], p, bid, off, lofs);
                 }
             };
 
-            auto compute_step = [&](const Tile<KV, D>(&cur)[kTilesPerIter], int it) {
-                float sc[kTilesPerIter][4];
+            // FULL: every tile of the step is a valid block lying wholly below `end`,
+            // so no masking code runs (the common case).
+            auto compute_step = [&](const Tile<KV, D>(&cur)[TPS], int it, auto full_tag) {
+                constexpr bool FULL = decltype(full_tag)::value;
+                float sc[TPS][4];
                 float mx = kMaxSeed;
 #pragma unroll
-                for (int j = 0; j < kTilesPerIter; ++j) {
-                    const int tt = it * kTilesPerIter + j;
+                for (int j = 0; j < TPS; ++j) {
+                    const int tt = it * TPS + j;
                     const int bid = tt < ntiles ? __builtin_amdgcn_readlane(my_bid, tt & 63) : -1;
                     const int pos0 = (ch + tt) * kTile;
-                    const bool full = bid >= 0 && pos0 + kTile <= end;  // wave-uniform
+                    const bool full = FULL || (bid >= 0 && pos0 + kTile <= end);  // wave-uniform
                     f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int cc = 0; cc < NC32; ++cc)
@@ -409,7 +493,7 @@ void decode_mfma_kernel(DecodeParams p) {
                 }
                 float lsum = 0.f;
 #pragma unroll
-                for (int j = 0; j < kTilesPerIter; ++j) {
+                for (int j = 0; j < TPS; ++j) {
                     h4 pa;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
@@ -430,18 +514,30 @@ void decode_mfma_kernel(DecodeParams p) {
                 l_run = l_run * alpha + lsum;
             };
 
-            // Two register buffers in ping-pong: step it+1 is in flight while
-            // step it computes; no buffer is copied (a copy would wait on its
-            // loads).  Steps past the end load zero-sized (free) tiles.
-            Tile<KV, D> buf_a[kTilesPerIter], buf_b[kTilesPerIter];
-            const int niters = (ntiles + kTilesPerIter - 1) / kTilesPerIter;
-            load_step(buf_a, 0);
-            for (int it = 0; it < niters; it += 2) {
-                load_step(buf_b, it + 1);
-                compute_step(buf_a, it);
-                if (it + 1 >= niters) break;
-                load_step(buf_a, it + 2);
-                compute_step(buf_b, it + 1);
+            // NBUF register buffers in rotation: steps it+1 .. it+NBUF-1 are in
+            // flight while step it computes; no buffer is copied (a copy would
+            // wait on its loads).  Steps past the end load zero-sized (free) tiles.
+            Tile<KV, D> buf[NBUF][TPS];
+            const int niters = (ntiles + TPS - 1) / TPS;
+            // Whole steps of valid blocks below `end` (tiles are in order).
+            int nfull = 0;
+            {
+                const int last_ok = (ch * kTile + ntiles * kTile <= end);
+                const bool all_valid = __builtin_amdgcn_read_exec() ==
+                                       (uint64_t)__ballot(lane >= ntiles || my_bid >= 0);
+                const int full_tiles = all_valid ? (last_ok ? ntiles : ntiles - 1) : 0;
+                nfull = full_tiles / TPS;
+            }
+#pragma unroll
+            for (int k = 0; k < NBUF - 1; ++k) load_step(buf[k], k);
+            for (int it = 0; it < niters; it += NBUF) {
+#pragma unroll
+                for (int k = 0; k < NBUF; ++k) {
+                    if (it + k >= niters) break;
+                    load_step(buf[(k + NBUF - 1) % NBUF], it + k + NBUF - 1);
+                    if (it + k < nfull) compute_step(buf[k], it + k, std::true_type{});
+                    else compute_step(buf[k], it + k, std::false_type{});
+                }
             }
         }
 
@@ -471,79 +567,71 @@ void decode_mfma_kernel(DecodeParams p) {
 #pragma unroll
                     for (int t = 0; t < NT; ++t) orow[16 * t + c] = o[t][r] * inv;
                 } else {
-                    const int64_t idx = ((int64_t)w * 2 + slot) * p.num_heads + head;
-                    float* orow = p.ws_o + idx * D;
+                    const int64_t blk = ((int64_t)w * 2 + slot) * p.pairs + pair;
+                    float* orow = p.ws_o + (blk * 8 + h) * D;
 #pragma unroll
                     for (int t = 0; t < NT; ++t) orow[16 * t + c] = o[t][r];
-                    if (c == 0) p.ws_ml[idx] = make_float2(mh[r], lh[r]);
+                    if (c == 0) p.ws_ml[blk * 16 + h] = make_float2(mh[r], lh[r]);
                 }
             }
         }
+    };
+
+    int carry = 0;
+    for (int base = 0; base < p.num_seqs; base += 64) {
+        const int sl = base + lane;
+        const int nt = sl < p.num_seqs ? tiles_of(p, sl) : 0;
+        const int Sl = carry + wave_excl_scan(nt, lane);
+        carry += wave_sum(nt);
+        const bool overlap = a < b && sl < p.num_seqs && nt > 0 && Sl < b && Sl + nt > a;
+        const bool zero_here = sl < p.num_seqs && nt == 0 &&
+                               ((Sl >= a && Sl < b) || (zero_owner_tail && Sl >= T));
+        uint64_t todo = __ballot(overlap || zero_here);
+        while (todo) {
+            const int j = __builtin_ctzll(todo);
+            todo &= todo - 1;
+            const int s = base + j;
+            // readlane keeps S / E in scalar registers: everything derived
+            // from them (tile counts, buffer descriptors) stays provably
+            // uniform, with no per-load waterfall loops.
+            const int S = __builtin_amdgcn_readlane(Sl, j);
+            const int E = S + __builtin_amdgcn_readlane(nt, j);
+            if (E == S) {  // no tiles: zero output
+                float* orow = p.out + ((int64_t)s * p.num_heads + head_base) * D;
+                for (int e = lane; e < gc * D; e += 64) orow[e] = 0.f;
+                continue;
+            }
+            process_fragment(s, S, E);
+        }
+        if (carry >= b && !zero_owner_tail) break;
     }
 }
 
-// Log-sum-exp merge of the fragments of one (sequence, head) per wave, and
-// zeros for sequences without tiles.  Fragment order: the first range holds
-// the sequence in slot 1, every later range in slot 0.
+// One wave per (sequence, kv-head slot): sequences split over several ranges
+// get their partial blocks merged; everything else was finished in place.
+template <int D>
 __global__ __launch_bounds__(256) void merge_split_kernel(DecodeParams p) {
-    const int lane = threadIdx.x & 63;
-    const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
+    __shared__ float wts_all[4][80];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int pair = blockIdx.y * 4 + wave;
     const int s = blockIdx.x;
-    if (head >= p.num_heads) return;
-    const int D = p.head_dim;
-    float* out = p.out + ((int64_t)s * p.num_heads + head) * D;
-    const int S = p.tile_start[s], E = p.tile_start[s + 1], T = p.tile_start[p.num_seqs];
-    if (E <= S) {
-        for (int d = lane; d < D; d += 64) out[d] = 0.f;
-        return;
-    }
+    if (pair >= p.pairs) return;
     const int G = p.num_wg;
-    // range holding tile t: the largest w with floor(w T / G) <= t
-    const int w0 = (int)(((int64_t)(S + 1) * G - 1) / T);
-    const int w1 = (int)(((int64_t)E * G - 1) / T);
+    int T = 0, S = 0;
+    for (int base = 0; base < p.num_seqs; base += 64) {
+        const int sl = base + lane;
+        const int nt = sl < p.num_seqs ? tiles_of(p, sl) : 0;
+        T += wave_sum(nt);
+        S += wave_sum(sl < s ? nt : 0);
+    }
+    const int E = S + tiles_of(p, s);
+    if (E <= S) return;  // no tiles: zeroed by the decode kernel
+    const int w0 = range_of(S, T, G), w1 = range_of(E - 1, T, G);
     if (w0 == w1) return;  // finished in place
-    const int nf = w1 - w0 + 1;
-    auto frag = [&](int i) -> int64_t {
-        return ((int64_t)(w0 + i) * 2 + (i == 0 ? 1 : 0)) * p.num_heads + head;
-    };
-    // A range can be empty when there are fewer tiles than ranges; it wrote
-    // nothing, so its slot holds stale data and must not take part.
-    auto live = [&](int i) -> bool {
-        return i < nf && range_start(w0 + i, T, G) < range_start(w0 + i + 1, T, G);
-    };
-    float M = kMaxSeed, L = 0.f;
-    for (int i0 = 0; i0 < nf; i0 += 64) {
-        const int i = i0 + lane;
-        float2 ml = make_float2(kMaxSeed, 0.f);
-        if (live(i)) ml = p.ws_ml[frag(i)];
-        float m = ml.x;
-        for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, shfl_xor(m, k));
-        const float Mn = fmaxf(M, m);
-        float l = fast_exp2(ml.x - Mn) * ml.y;
-        for (int k = 32; k >= 1; k >>= 1) l += shfl_xor(l, k);
-        L = L * fast_exp2(M - Mn) + l;
-        M = Mn;
-    }
-    const float inv = 1.0f / (L + 1e-9f);
-    // Weights are broadcast with readlane (EXEC-independent); the d loop may
-    // leave lanes inactive when head_dim is not a multiple of 64.
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // d = lane + 64 k, head_dim <= 256
-    for (int i0 = 0; i0 < nf; i0 += 64) {
-        const int n = min(64, nf - i0);
-        float wt = 0.f;
-        if (live(i0 + lane)) wt = fast_exp2(p.ws_ml[frag(i0 + lane)].x - M);
-        for (int j = 0; j < n; ++j) {
-            const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wt), j));
-            if (wj == 0.f) continue;  // empty range or negligible weight (uniform)
-            const float* orow = p.ws_o + frag(i0 + j) * D;
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                if (lane + 64 * k < D) acc[k] += wj * orow[lane + 64 * k];
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-        if (lane + 64 * k < D) out[lane + 64 * k] = acc[k] * inv;
+    const int kvh = pair / p.qchunks, qc = pair - kvh * p.qchunks;
+    merge_fragments<D>(p, s, w0, w1, pair, kvh * p.group + qc * 8, min(8, p.group - qc * 8), T,
+                       lane, reinterpret_cast<__attribute__((address_space(3))) float*>(
+                                 (__attribute__((address_space(3))) float*)wts_all[wave]));
 }
 
 // ---- fp32 pages -----------------------------------------------------------
@@ -670,13 +758,28 @@ __global__ __launch_bounds__(256) void merge_parts_kernel(DecodeParams p) {
         if (lane + 64 * k < D) out[lane + 64 * k] = acc[k] * inv;
 }
 
-template <int KV, int D>
-hipError_t launch_mfma(const DecodeParams& p, hipStream_t stream) {
+template <int KV, int D, int TPS, int NBUF>
+hipError_t launch_shape(const DecodeParams& p, hipStream_t stream) {
     const int wpw = p.pairs < kWavesPerGroup ? p.pairs : kWavesPerGroup;
     dim3 grid(p.num_wg, (p.pairs + wpw - 1) / wpw);
-    const size_t lds = (size_t)wpw * kTilesPerIter * kTile * D * sizeof(_Float16);
-    hipLaunchKernelGGL((decode_mfma_kernel<KV, D>), grid, dim3(wpw * 64), lds, stream, p);
+    const size_t lds = (size_t)wpw * TPS * kTile * D * sizeof(_Float16);
+    hipLaunchKernelGGL((decode_mfma_kernel<KV, D, TPS, NBUF>), grid, dim3(wpw * 64), lds, stream, p);
     return hipGetLastError();
+}
+
+template <int KV, int D>
+hipError_t launch_mfma(const DecodeParams& p, hipStream_t stream) {
+    switch (p.pipeline) {
+        case 2: return launch_shape<KV, D, 2, 4>(p, stream);
+        case 3: return launch_shape<KV, D, 1, 6>(p, stream);
+        case 4: return launch_shape<KV, D, 1, 8>(p, stream);
+        case 5: return launch_shape<KV, D, 4, 2>(p, stream);
+        default:
+            // 2 tiles x 3 buffers fits 256 VGPRs without spills up to
+            // head_dim 80; wider heads take 1 tile x 4 buffers.
+            if constexpr (D <= 80) return launch_shape<KV, D, 2, 3>(p, stream);
+            else return launch_shape<KV, D, 1, 4>(p, stream);
+    }
 }
 
 }  // namespace
@@ -707,9 +810,6 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
         }
         return err;
     }
-    hipLaunchKernelGGL(split_scan_kernel, dim3(1), dim3(1024), 0, stream, p);
-    err = hipGetLastError();
-    if (err != hipSuccess) return err;
     if (prof) prof_begin(kKernelDecode, stream);
 #define VCPP_DISPATCH_D(KVT)                                              \
     switch (p.head_dim) {                                                 \
@@ -727,8 +827,12 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
     if (err != hipSuccess) return err;
     if (prof) prof_end(kKernelDecode, stream);
     if (prof) prof_begin(kKernelMerge, stream);
-    dim3 mg(p.num_seqs, (p.num_heads + 3) / 4);
-    hipLaunchKernelGGL(merge_split_kernel, mg, dim3(256), 0, stream, p);
+    dim3 mg(p.num_seqs, (p.pairs + 3) / 4);
+    switch (p.head_dim) {
+        case 64: hipLaunchKernelGGL(merge_split_kernel<64>, mg, dim3(256), 0, stream, p); break;
+        case 80: hipLaunchKernelGGL(merge_split_kernel<80>, mg, dim3(256), 0, stream, p); break;
+        default: hipLaunchKernelGGL(merge_split_kernel<128>, mg, dim3(256), 0, stream, p); break;
+    }
     err = hipGetLastError();
     if (prof) prof_end(kKernelMerge, stream);
     return err;

@@ -124,14 +124,15 @@ def decode_workspace_size(pages, num_seqs, num_heads, max_context_len, partition
 
 def paged_decode(pages, q, out, block_tables, context_lens, max_context_len, num_heads,
                  table_lens=None, partition_size=0, workspace=None, stream=None):
-    """vcpp_paged_decode on device tensors.  `workspace` is a uint8 device tensor
-    of at least decode_workspace_size(...) bytes (allocated here when None)."""
+    """vcpp_paged_decode on device tensors.  `workspace` is a zero-initialised
+    uint8 device tensor of at least decode_workspace_size(...) bytes, reused
+    across calls (allocated here when None)."""
     num_seqs = q.shape[0]
     max_blocks = block_tables.shape[1] if block_tables is not None and block_tables.dim() == 2 else 0
     need = decode_workspace_size(pages, num_seqs, num_heads, max_context_len, partition_size)
     if workspace is None and need > 0:
         import torch
-        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        workspace = torch.zeros(need, dtype=torch.uint8, device=q.device)
     ws_bytes = workspace.numel() if workspace is not None else 0
     rc = lib().vcpp_paged_decode(ctypes.byref(pages), _ptr(q), _ptr(out), _ptr(block_tables),
                                  max_blocks, _ptr(table_lens), _ptr(context_lens), num_seqs,
