@@ -41,6 +41,9 @@ def parse():
                     help="target CPU time of the baseline sample")
     ap.add_argument("--partition", type=int, default=0,
                     help="split-K partition size (0 = library default)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a device-to-device copy of 1 GiB five times (the known-size "
+                         "kernel that rocprofv3 FETCH_SIZE / WRITE_SIZE readings are scaled by)")
     return ap.parse_args()
 
 
@@ -149,6 +152,15 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     pyvcpp.lib()
+    if args.copy_calibration:
+        x = torch.empty(1 << 29, dtype=torch.float16, device="cuda:0").fill_(1.0)
+        y = torch.empty_like(x)
+        for _ in range(5):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": x.numel() * 2, "copy_bytes_written": y.numel() * 2,
+                          "launches": 5}))
+        return
 
     w = decode_workload(torch, args.seed)
     pages0 = pyvcpp.kv_pages(pyvcpp.KV_F16, w["sets"][0][0], w["sets"][0][1], BS, HKV, D, w["nb"],

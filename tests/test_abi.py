@@ -1,0 +1,90 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+include/*.h declares, and rejects bad arguments with a status code and a
+message (argument validation runs before any HIP call)."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+import pyvcpp
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b([A-Za-z_]\w*)\s*\(", text, re.M):
+            name = m.group(1)
+            if name not in ("if", "while", "sizeof", "defined"):
+                names.add(name)
+    return names
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    L = pyvcpp.lib()
+    names = declared_functions()
+    assert "vcpp_paged_decode" in names and "paged_attention_cuda" in names
+    for n in sorted(names):
+        assert hasattr(L, n), "missing export %s" % n
+    assert set(pyvcpp.EXPORTS) <= names
+
+
+def test_version_and_error_string():
+    assert b"gfx950" in pyvcpp.lib().vcpp_version()
+    assert isinstance(pyvcpp.last_error(), str)
+
+
+class FakeTensor:
+    def __init__(self, addr, shape=(1,)):
+        self._addr = addr
+        self.shape = shape
+
+    def data_ptr(self):
+        return self._addr
+
+
+def pages(dtype=pyvcpp.KV_F16, block_size=16, hkv=8, d=80, nb=10, stride=None, k=4096, v=8192):
+    stride = block_size * hkv * d if stride is None else stride
+    return pyvcpp.KVPages(dtype, block_size, hkv, d, nb, stride, 0, k, v, None, None)
+
+
+def call(pg, num_seqs=1, num_heads=64, max_ctx=16, partition=0, q=4096, out=4096, ctx=4096,
+         tables=4096, max_blocks=1, ws=None, ws_bytes=0):
+    L = pyvcpp.lib()
+    return L.vcpp_paged_decode(ctypes.byref(pg), q, out, tables, max_blocks, None, ctx, num_seqs,
+                               max_ctx, num_heads, partition, ws, ws_bytes, None)
+
+
+@pytest.mark.parametrize("kwargs,code,frag", [
+    (dict(pg=pages(block_size=8)), pyvcpp.VCPP_E_UNSUPPORTED, "block_size"),
+    (dict(pg=pages(d=72)), pyvcpp.VCPP_E_UNSUPPORTED, "head_dim"),
+    (dict(pg=pages(dtype=7)), pyvcpp.VCPP_E_INVALID, "dtype"),
+    (dict(pg=pages(), num_heads=60), pyvcpp.VCPP_E_INVALID, "num_heads"),
+    (dict(pg=pages(), partition=24), pyvcpp.VCPP_E_INVALID, "partition"),
+    (dict(pg=pages(k=4097)), pyvcpp.VCPP_E_INVALID, "aligned"),
+    (dict(pg=pages(stride=16 * 8 * 80 - 8)), pyvcpp.VCPP_E_INVALID, "block_stride"),
+    (dict(pg=pages(), q=None), pyvcpp.VCPP_E_INVALID, "NULL"),
+    (dict(pg=pages(), max_ctx=100000, num_seqs=4), pyvcpp.VCPP_E_WORKSPACE, "workspace"),
+    (dict(pg=pages(dtype=pyvcpp.KV_I8)), pyvcpp.VCPP_E_INVALID, "scale"),
+])
+def test_argument_errors(kwargs, code, frag):
+    rc = call(**kwargs)
+    assert rc == code
+    assert frag in pyvcpp.last_error()
+
+
+def test_empty_batch_is_a_no_op():
+    assert call(pages(), num_seqs=0) == pyvcpp.VCPP_OK
+    assert pyvcpp.last_error() == ""
+
+
+def test_v1_rejects_block_size():
+    L = pyvcpp.lib()
+    ctx = (ctypes.c_int32 * 1)(16)
+    L.paged_attention_cuda(4096, 4096, 4096, ctypes.addressof(ctx), 4096, 64, 8, 80, 8, 1)
+    assert "block_size" in pyvcpp.last_error()
