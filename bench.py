@@ -41,6 +41,8 @@ def parse():
                     help="target CPU time of the baseline sample")
     ap.add_argument("--partition", type=int, default=0,
                     help="split-K partition size (0 = library default)")
+    ap.add_argument("--prefill-steps", type=int, default=20)
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill leg")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a device-to-device copy of 1 GiB five times (the known-size "
                          "kernel that rocprofv3 FETCH_SIZE / WRITE_SIZE readings are scaled by)")
@@ -87,6 +89,74 @@ def run_decode_steps(torch, pyvcpp, w, steps, workspace, partition=0):
         j = i % len(pages)
         pyvcpp.paged_decode(pages[j], w["q"], w["out"], w["sets"][j][2], w["ctx_dev"],
                             w["max_ctx"], H, workspace=workspace, partition_size=partition)
+
+
+# ---------------------------------------------------------------------------
+# prefill workload (config 3)
+
+def prefill_workload(torch, seed):
+    """8 chunks x 2048 new tokens appended to 1024-token paged prefixes, 64/8
+    heads, head_dim 80, fp16 Q/K/V ~ N(0, 0.5), block_size 16, random tables."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    chunks, new, prefix = 8, 2048, 1024
+    total = prefix + new
+    nblk = (total + BS - 1) // BS
+    nb = chunks * nblk
+    dev = torch.device("cuda:0")
+    gd = torch.Generator(device=dev).manual_seed(seed + 1)
+    k = (0.5 * torch.randn((nb, BS, HKV, D), generator=gd, device=dev)).half()
+    v = (0.5 * torch.randn((nb, BS, HKV, D), generator=gd, device=dev)).half()
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    tables = perm.view(chunks, nblk).to(dev)
+    q = (0.5 * torch.randn((chunks * new, H, D), generator=gd, device=dev)).half()
+    out = torch.empty((chunks * new, H, D), dtype=torch.float32, device=dev)
+    q_start = torch.arange(0, chunks * new + 1, new, dtype=torch.int32, device=dev)
+    pre = torch.full((chunks,), prefix, dtype=torch.int32, device=dev)
+    pairs = chunks * sum(prefix + i + 1 for i in range(new))
+    flops = 4 * D * H * pairs
+    return dict(k=k, v=v, tables=tables, q=q, out=out, q_start=q_start, prefix=pre, nb=nb,
+                new=new, flops=flops, chunks=chunks, prefix_len=prefix)
+
+
+def run_prefill_steps(pyvcpp, pw, steps):
+    pages = pyvcpp.kv_pages(pyvcpp.KV_F16, pw["k"], pw["v"], BS, HKV, D, pw["nb"], BS * HKV * D)
+    for _ in range(steps):
+        pyvcpp.paged_prefill(pages, pw["q"], pw["out"], pw["tables"], pw["q_start"], pw["prefix"],
+                             pw["new"], H)
+
+
+def bench_prefill(torch, pyvcpp, args):
+    pw = prefill_workload(torch, args.seed + 7)
+    run_prefill_steps(pyvcpp, pw, 3)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run_prefill_steps(pyvcpp, pw, args.prefill_steps)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.prefill_steps
+    pyvcpp.profile_enable(True)
+    run_prefill_steps(pyvcpp, pw, args.prefill_steps)
+    torch.cuda.synchronize()
+    ms, n = pyvcpp.profile_read(pyvcpp.KERNEL_PREFILL)
+    pyvcpp.profile_enable(False)
+    k_s = ms / max(n, 1) / 1e3
+    value = pw["flops"] / dt / 1e12
+    achieved = pw["flops"] / k_s / 1e12
+    return {
+        "metric": "prefill attn TFLOP/s",
+        "value": round(value, 2), "unit": "TFLOP/s", "steps": args.prefill_steps,
+        "ms_per_step": round(dt * 1e3, 4),
+        "pct_of_mfma_peak": round(100 * value / F16_MFMA_PEAK_TFS, 2),
+        "dtype": "f16 Q/K/V, fp32 accumulate, fp32 out",
+        "config": {"workload": "BASELINE config 3: 8 chunks x 2048 new tokens on 1024-token paged "
+                               "prefixes, causal, 64 q / 8 kv heads, head_dim 80, fp16 N(0,0.5)",
+                   "flops_per_step": pw["flops"],
+                   "flop_count": "4*D*H per causal-valid (query, key) pair"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": F16_MFMA_PEAK_TFS,
+                     "unit": "TFLOP/s", "frac": round(achieved / F16_MFMA_PEAK_TFS, 4),
+                     "traffic": read_traffic("prefill_mfma_config3_traffic.txt"),
+                     "kernel": "prefill_mfma_kernel<f16,80>",
+                     "kernel_avg_us": round(k_s * 1e6, 1)},
+    }
 
 
 # ---------------------------------------------------------------------------
@@ -213,6 +283,8 @@ def main():
                      "merge_avg_us": round(mrg_ms / max(mrg_n, 1) * 1e3, 2)},
         "prefill": None,
     }
+    if not args.no_prefill:
+        result["prefill"] = bench_prefill(torch, pyvcpp, args)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(torch, w, args.cpu_seconds)
     else:

@@ -118,6 +118,32 @@ int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
 size_t vcpp_decode_workspace_size(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_heads,
                                   int32_t max_context_len, int32_t partition_size);
 
+/* ---- v2: chunked causal prefill ---------------------------------------- */
+
+/*
+ * Causal attention of chunks of new tokens appended to paged prefixes.  Chunk
+ * c owns query rows q_start[c] .. q_start[c+1]-1; row i of the chunk attends
+ * positions 0 .. prefix_lens[c] + i of its sequence through table row c --
+ * the engine's per-position prefill (src/paged_engine.cpp:348-384,
+ * src/model.cpp:1214-1220) done for the whole chunk at once.  The chunk's own
+ * K/V must already be in the pages (written before the call, as the engine
+ * does).
+ *   q            fp16 (binary16 bits) [total_rows][num_heads][head_dim]
+ *   out          fp32 [total_rows][num_heads][head_dim] (overwritten)
+ *   block_tables [num_chunks][max_blocks_per_seq] int32
+ *   q_start      [num_chunks + 1] int32 on the device (q_start[0] == 0)
+ *   prefix_lens  [num_chunks] int32 on the device
+ *   max_chunk_len host-side upper bound of the chunk lengths (sizes the grid)
+ * KV dtypes: VCPP_KV_F16 and VCPP_KV_I8 (int8 is dequantised to fp16 on the
+ * way into LDS); head_dim 64, 80 or 128; num_heads / num_kv_heads any.
+ * Replaces read_kv_prefill + compute_attention per position
+ * (src/paged_attention.cpp:174-201, src/paged_engine.cpp:64-113,381-384).
+ */
+int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
+                       const int32_t* block_tables, int32_t max_blocks_per_seq,
+                       const int32_t* q_start, const int32_t* prefix_lens, int32_t num_chunks,
+                       int32_t max_chunk_len, int32_t num_heads, void* stream);
+
 /* ---- v1: reference launcher signatures (cuda/attention.h) -------------- */
 
 /*

@@ -51,3 +51,40 @@ def assert_close(got, want, atol, rtol, what=""):
     bad = err > atol + rtol * np.abs(want)
     assert not bad.any(), "%s: %d/%d out of tolerance, max abs err %.3g at %s" % (
         what, int(bad.sum()), bad.size, err.max(), np.unravel_index(err.argmax(), err.shape))
+
+
+def prefill_tables(seed, lens, num_blocks, bs=16):
+    """Random disjoint block tables for sequences of `lens` tokens."""
+    from oracle_lib import permutation
+    nbs = [(n + bs - 1) // bs for n in lens]
+    mb = max(max(nbs), 1)
+    perm = permutation(seed, num_blocks)
+    t = np.full((len(lens), mb), -1, dtype=np.int32)
+    k = 0
+    for i, n in enumerate(nbs):
+        t[i, :n] = perm[k:k + n]
+        k += n
+    assert k <= num_blocks
+    return t
+
+
+def gpu_prefill(dpool, q16, tables, q_start, prefix, num_heads):
+    """q16: uint16 fp16 bits [rows][H][D]."""
+    qd = dev(q16)
+    out = torch.full(q16.shape, float("nan"), dtype=torch.float32, device="cuda:0")
+    lens = np.diff(q_start)
+    pyvcpp.paged_prefill(dpool.pages, qd, out, dev(np.asarray(tables, np.int32)),
+                         dev(np.asarray(q_start, np.int32)), dev(np.asarray(prefix, np.int32)),
+                         int(lens.max()) if len(lens) else 0, num_heads)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def oracle_prefill_rows(pool, q32, tables, q_start, prefix, num_heads, rows, nthreads=8):
+    """Oracle for selected query rows only: each row is a single-token query
+    over positions 0..prefix+i of its chunk (the engine's per-position
+    semantics), evaluated with the batched decode oracle."""
+    from oracle_lib import decode
+    chunk_of = np.searchsorted(q_start, rows, side="right") - 1
+    ctx = np.array([prefix[c] + (r - q_start[c]) + 1 for r, c in zip(rows, chunk_of)], np.int32)
+    return decode(pool, q32[rows], tables[chunk_of], ctx, num_heads, nthreads=nthreads)

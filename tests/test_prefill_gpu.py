@@ -1,0 +1,83 @@
+"""GPU parity of the chunked causal prefill path (vcpp_paged_prefill) against
+the CPU oracle's per-position semantics on identical seeded inputs.
+
+Tolerance (numpy allclose form): atol 2e-3, rtol 1e-2 for fp16 and int8 pages.
+q is fp16 on the GPU; the oracle gets the same fp16 values as fp32.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from gpu_util import (DevPool, assert_close, gpu_prefill, oracle_prefill_rows, prefill_tables)
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def make_case(kind, seed, prefix, chunk, H, Hkv, D=80, std=1.0, extra_blocks=8):
+    lens = [p + n for p, n in zip(prefix, chunk)]
+    nb = sum((l + 15) // 16 for l in lens) + extra_blocks
+    pool = O.make_pool(kind, seed, nb, Hkv, D, 0.0, std)
+    q_start = np.concatenate([[0], np.cumsum(chunk)]).astype(np.int32)
+    q32 = O.normal(seed + 7, (int(q_start[-1]), H, D), 0.0, std)
+    q16 = q32.astype(np.float16)
+    tables = prefill_tables(seed + 11, lens, nb)
+    return pool, q16, q16.astype(np.float32), tables, q_start, np.array(prefix, np.int32)
+
+
+@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8])
+@pytest.mark.parametrize("heads", [(64, 8), (8, 1), (32, 2), (16, 16)])
+def test_prefill_small(cuda, kind, heads):
+    H, Hkv = heads
+    prefix = [0, 19, 1, 64, 200, 0]
+    chunk = [1, 21, 64, 65, 37, 130]
+    pool, q16, q32, tables, q_start, pre = make_case(kind, 500 + H, prefix, chunk, H, Hkv)
+    want = O.prefill(pool, q32, tables, q_start, pre, H)
+    got = gpu_prefill(DevPool(pool), q16, tables, q_start, pre, H)
+    assert_close(got, want, ATOL, RTOL, what="prefill H=%d Hkv=%d kind=%d" % (H, Hkv, kind))
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_prefill_head_dims(cuda, D):
+    prefix, chunk = [7, 100], [90, 33]
+    pool, q16, q32, tables, q_start, pre = make_case(O.ORC_F16, 610 + D, prefix, chunk, 64, 8, D)
+    want = O.prefill(pool, q32, tables, q_start, pre, 64)
+    got = gpu_prefill(DevPool(pool), q16, tables, q_start, pre, 64)
+    assert_close(got, want, ATOL, RTOL, what="prefill D=%d" % D)
+
+
+def test_prefill_skips_invalid_blocks(cuda):
+    prefix, chunk = [48, 0], [40, 70]
+    pool, q16, q32, tables, q_start, pre = make_case(O.ORC_F16, 620, prefix, chunk, 64, 8)
+    tables[0, 1] = -1          # a prefix page missing
+    tables[1, 2] = 10 ** 6     # an id past the pool
+    want = O.prefill(pool, q32, tables, q_start, pre, 64)
+    got = gpu_prefill(DevPool(pool), q16, tables, q_start, pre, 64)
+    assert_close(got, want, ATOL, RTOL, what="prefill invalid blocks")
+
+
+def test_prefill_matches_decode_for_single_token_chunks(cuda):
+    """A chunk of one token on a prefix is a decode step (same oracle row)."""
+    prefix, chunk = [300, 17, 1000], [1, 1, 1]
+    pool, q16, q32, tables, q_start, pre = make_case(O.ORC_F16, 630, prefix, chunk, 64, 8)
+    ctx = pre + 1
+    want = O.decode(pool, q32, tables, ctx, 64)
+    got = gpu_prefill(DevPool(pool), q16, tables, q_start, pre, 64)
+    assert_close(got, want, ATOL, RTOL, what="prefill as decode")
+
+
+def test_prefill_config3_sampled(cuda):
+    """BASELINE config 3 at full size: 8 chunks x 2048 new tokens on 1024-token
+    paged prefixes, 64/8 heads, head_dim 80, fp16 N(0, 0.5); all rows run on
+    the GPU, 96 random rows (and the first/last of each chunk) are checked."""
+    prefix, chunk = [1024] * 8, [2048] * 8
+    pool, q16, q32, tables, q_start, pre = make_case(O.ORC_F16, 640, prefix, chunk, 64, 8,
+                                                     std=0.5)
+    got = gpu_prefill(DevPool(pool), q16, tables, q_start, pre, 64)
+    assert np.all(np.isfinite(got))
+    rng = np.random.default_rng(7)
+    rows = np.unique(np.concatenate([rng.integers(0, q_start[-1], 96), q_start[:-1],
+                                     q_start[1:] - 1]))
+    want = oracle_prefill_rows(pool, q32, tables, q_start, pre, 64, rows)
+    assert_close(got[rows], want, ATOL, RTOL, what="config3 rows")

@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "decode.h"
+#include "prefill.h"
 #include "vcpp_attention.h"
 
 namespace {
@@ -248,6 +249,59 @@ int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
     if (p.pairs > 65535 * 8) return fail(VCPP_E_UNSUPPORTED, "too many kv heads");
     hipError_t e = vcpp::launch_decode(p, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "decode launch");
+    return VCPP_OK;
+}
+
+int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
+                       const int32_t* block_tables, int32_t max_blocks_per_seq,
+                       const int32_t* q_start, const int32_t* prefix_lens, int32_t num_chunks,
+                       int32_t max_chunk_len, int32_t num_heads, void* stream) {
+    g_last_error.clear();
+    int rc = check_pages(kv);
+    if (rc != VCPP_OK) return rc;
+    if (kv->dtype == VCPP_KV_F32)
+        return fail(VCPP_E_UNSUPPORTED, "prefill supports fp16 and int8 pages (got fp32)");
+    if (kv->head_dim != 64 && kv->head_dim != 80 && kv->head_dim != 128)
+        return fail(VCPP_E_UNSUPPORTED, "prefill head_dim %d (64, 80 or 128)", kv->head_dim);
+    if (num_chunks < 0 || max_chunk_len < 0)
+        return fail(VCPP_E_INVALID, "num_chunks and max_chunk_len must be >= 0");
+    if (num_chunks == 0 || max_chunk_len == 0) return VCPP_OK;
+    if (!q || !out || !q_start || !prefix_lens)
+        return fail(VCPP_E_INVALID, "q/out/q_start/prefix_lens is NULL");
+    if (max_blocks_per_seq <= 0 || !block_tables)
+        return fail(VCPP_E_INVALID, "block_tables missing");
+    if (num_heads <= 0 || num_heads % kv->num_kv_heads != 0)
+        return fail(VCPP_E_INVALID, "num_heads %d is not a positive multiple of num_kv_heads %d",
+                    num_heads, kv->num_kv_heads);
+    if (num_chunks > 65535) return fail(VCPP_E_UNSUPPORTED, "too many chunks (%d)", num_chunks);
+    vcpp::PrefillParams p{};
+    p.k = kv->k;
+    p.v = kv->v;
+    p.k_scale = kv->k_scale;
+    p.v_scale = kv->v_scale;
+    p.num_blocks = kv->num_blocks;
+    p.block_stride = kv->block_stride;
+    p.scale_block_stride = kv->scale_block_stride;
+    p.block_size = kv->block_size;
+    p.num_kv_heads = kv->num_kv_heads;
+    p.head_dim = kv->head_dim;
+    p.kv_dtype = kv->dtype;
+    p.q = q;
+    p.out = out;
+    p.num_heads = num_heads;
+    p.group = num_heads / kv->num_kv_heads;
+    p.head_groups = vcpp::prefill_head_groups(p.group);
+    if ((int64_t)kv->num_kv_heads * p.head_groups > 65535)
+        return fail(VCPP_E_UNSUPPORTED, "too many heads");
+    p.block_tables = block_tables;
+    p.q_start = q_start;
+    p.prefix_lens = prefix_lens;
+    p.max_blocks = max_blocks_per_seq;
+    p.num_chunks = num_chunks;
+    p.max_chunk_len = max_chunk_len;
+    p.scale_log2 = (1.0f / std::sqrt((float)kv->head_dim)) * 1.4426950408889634f;
+    hipError_t e = vcpp::launch_prefill(p, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "prefill launch");
     return VCPP_OK;
 }
 

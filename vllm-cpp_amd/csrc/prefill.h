@@ -1,0 +1,43 @@
+// prefill.h -- internal launch interface of the chunked prefill kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vcpp_attention.h"
+
+namespace vcpp {
+
+struct PrefillParams {
+    // KV pages (see vcpp_kv_pages)
+    const void* k;
+    const void* v;
+    const uint16_t* k_scale;
+    const uint16_t* v_scale;
+    int64_t num_blocks;
+    int64_t block_stride;
+    int64_t scale_block_stride;
+    int32_t block_size;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t kv_dtype;
+    // queries (fp16 [rows][num_heads][head_dim]) and fp32 outputs
+    const uint16_t* q;
+    float* out;
+    int32_t num_heads;
+    int32_t group;        // num_heads / num_kv_heads
+    int32_t head_groups;  // workgroups per kv head (4 query heads each)
+    // chunks
+    const int32_t* block_tables;  // [num_chunks][max_blocks]
+    const int32_t* q_start;       // [num_chunks + 1] device
+    const int32_t* prefix_lens;   // [num_chunks] device
+    int32_t max_blocks;
+    int32_t num_chunks;
+    int32_t max_chunk_len;
+    float scale_log2;  // log2(e) / sqrt(head_dim)
+};
+
+hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream);
+int prefill_head_groups(int group);
+
+}  // namespace vcpp

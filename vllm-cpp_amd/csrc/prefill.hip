@@ -1,0 +1,339 @@
+// prefill.hip -- chunked causal prefill attention over paged K/V for gfx950.
+//
+// Reference semantics: the engine prefills one position at a time, writing
+// that position's K/V and attending over positions 0..pos
+// (src/paged_engine.cpp:348-384, src/model.cpp:1214-1220), i.e. query row i
+// of a chunk appended to a prefix of p tokens sees positions 0..p+i, through
+// the same paged softmax as src/paged_attention.cpp:11-90 (scale
+// 1/sqrt(head_dim), sum + 1e-9, invalid / missing blocks skipped).  The
+// reference's GPU slot for dense attention is flash_attention_cuda
+// (cuda/attention.cu:58-124); its host loops are not followed.
+//
+// Work decomposition: a workgroup = (16*RB-token query tile, chunk, kv head,
+// group of 4 query heads); one wave per query head holds RB row blocks of 16
+// query tokens.  Keys stream in blocks of 32 (two 16-token tiles) through
+// double-buffered LDS: the workgroup gathers each block's K and V rows of its
+// kv head through the block table with 16-byte loads (int8 pages are
+// dequantised to fp16 here).  Per row block and key block:
+//   S^T[32 keys][16 rows] = K_blk x Q^T    (16x16x32 f16; a 16-dim remainder
+//                                           as 16x16x16 into its own accumulator)
+//   O[16 rows][D | 16]  += P x [V_blk | 1] (16x16x32 f16, P straight from the
+//                                           S^T accumulator layout)
+// The all-ones extra column block yields the row sums of exactly the fp16 P
+// that multiplies V.  The running max is only moved (and O rescaled) when a
+// row's max grows by more than 2^8, so P stays <= 256 and most blocks skip
+// the rescale.  Causal masks are applied only on key blocks that reach past
+// the first query token of the tile.
+#include "device_common.h"
+#include "prefill.h"
+#include "profile.h"
+
+namespace vcpp {
+
+namespace {
+
+constexpr int kKBlk = 32;   // keys per block
+constexpr int kHeadsPerGroup = 4;
+constexpr float kLazy = 8.0f;  // log2 of the largest P allowed before rescaling
+
+typedef short s4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) char lds_char;
+
+template <int D>
+struct PDims {
+    static constexpr int NC32 = D / 32;
+    static constexpr int REM = (D % 32) / 16;
+    static constexpr int NT = D / 16;
+    static constexpr int RB = D <= 80 ? 4 : 2;  // 16-token row blocks per wave
+    static constexpr int QT = 16 * RB;          // query tokens per workgroup
+    static constexpr int CHUNKS = D / 8;        // 16-byte chunks per K/V row
+    // LDS row pitch: 16 bytes of padding make the 16-byte K fragment reads of
+    // 16 consecutive rows hit 16 distinct 4-bank groups.
+    static constexpr int PITCH = D * 2 + 16;
+};
+
+__device__ __forceinline__ h4 read_tr(lds_char* a) {
+    const s4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        reinterpret_cast<__attribute__((address_space(3))) s4*>(a));
+    return __builtin_bit_cast(h4, x);
+}
+
+__device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+
+// Gathers key block [key0, key0 + 32) of kv head kvh into LDS rows [key][D]
+// (K at kbuf, V at vbuf), zero rows for keys at or past kv_end or on invalid
+// blocks.  Thread t handles 16-byte chunks t, t + 256, ...
+template <int KV, int D>
+struct BlockLoader {
+    static constexpr int TOTAL = 2 * kKBlk * PDims<D>::CHUNKS;  // K then V chunks
+    static constexpr int PER = (TOTAL + 255) / 256;
+    h8 reg[PER];
+
+    __device__ __forceinline__ void load(const PrefillParams& p, const int32_t* table, int tlen,
+                                         int kvh, int key0, int kv_end, int tid) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int ci = tid + 256 * i;
+            h8 x = {};
+            if (ci < TOTAL) {
+                const int which = ci / (kKBlk * PDims<D>::CHUNKS);  // 0 K, 1 V
+                const int r = ci - which * kKBlk * PDims<D>::CHUNKS;
+                const int key = r / PDims<D>::CHUNKS, ch = r - key * PDims<D>::CHUNKS;
+                const int pos = key0 + key;
+                const int lb = pos / p.block_size;
+                if (pos < kv_end && lb < tlen) {
+                    const int bid = table[lb];
+                    if (bid >= 0 && (int64_t)bid < p.num_blocks) {
+                        const int slot = pos - lb * p.block_size;
+                        const int64_t e = (int64_t)bid * p.block_stride +
+                                          ((int64_t)slot * p.num_kv_heads + kvh) * D + ch * 8;
+                        if constexpr (KV == VCPP_KV_F16) {
+                            const _Float16* base = static_cast<const _Float16*>(which ? p.v : p.k);
+                            x = *reinterpret_cast<const h8*>(base + e);
+                        } else {
+                            const int8_t* base = static_cast<const int8_t*>(which ? p.v : p.k);
+                            const i2 raw = *reinterpret_cast<const i2*>(base + e);
+                            const uint16_t* sc = which ? p.v_scale : p.k_scale;
+                            const float s = h2f(sc[(int64_t)bid * p.scale_block_stride +
+                                                   (int64_t)kvh * p.block_size + slot]);
+                            const h8 q = i8x8_to_h8((uint32_t)raw.x, (uint32_t)raw.y);
+#pragma unroll
+                            for (int k = 0; k < 8; ++k) x[k] = (_Float16)((float)q[k] * s);
+                        }
+                    }
+                }
+            }
+            reg[i] = x;
+        }
+    }
+
+    __device__ __forceinline__ void store(lds_char* kbuf, lds_char* vbuf, int tid) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int ci = tid + 256 * i;
+            if (ci < TOTAL) {
+                const int which = ci / (kKBlk * PDims<D>::CHUNKS);
+                const int r = ci - which * kKBlk * PDims<D>::CHUNKS;
+                const int key = r / PDims<D>::CHUNKS, ch = r - key * PDims<D>::CHUNKS;
+                lds_char* dst = (which ? vbuf : kbuf) + key * PDims<D>::PITCH + ch * 16;
+                *reinterpret_cast<__attribute__((address_space(3))) h8*>(dst) = reg[i];
+            }
+        }
+    }
+};
+
+template <int KV, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_mfma_kernel(PrefillParams p) {
+    constexpr int NC32 = PDims<D>::NC32, NT = PDims<D>::NT, RB = PDims<D>::RB;
+    constexpr int kQTile = PDims<D>::QT;
+    constexpr int KROW = PDims<D>::PITCH;     // bytes per LDS row
+    constexpr int BUF = kKBlk * KROW;         // bytes of one K (or V) block
+    __shared__ __attribute__((aligned(16))) char lds_raw[4 * BUF];  // 2 x (K, V) blocks
+    lds_char* lds = reinterpret_cast<lds_char*>((__attribute__((address_space(3))) char*)lds_raw);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int chunk = blockIdx.y;
+    const int q0 = p.q_start[chunk], n = p.q_start[chunk + 1] - q0;
+    const int ntile = (n + kQTile - 1) / kQTile;
+    const int tile = ntile - 1 - (int)blockIdx.x;  // heaviest (latest) tiles first
+    if (tile < 0) return;                          // whole workgroup: before any barrier
+    const int t0 = tile * kQTile;
+    const int prefix = p.prefix_lens[chunk];
+    const int kvh = blockIdx.z / p.head_groups;
+    const int hg = blockIdx.z - kvh * p.head_groups;
+    const int hl = hg * kHeadsPerGroup + wave;  // head within the GQA group
+    const bool head_ok = hl < p.group;
+    const int head = kvh * p.group + (head_ok ? hl : 0);
+    const int32_t* table = p.block_tables + (int64_t)chunk * p.max_blocks;
+    const int tlen = p.max_blocks;
+    // Keys visible to the tile: positions < prefix + min(t0 + 64, n).
+    const int kv_end = prefix + min(t0 + kQTile, n);
+    const int nblk = (kv_end + kKBlk - 1) / kKBlk;
+    // Key blocks wholly visible to every row of the tile need no mask.
+    const int nfree = (prefix + t0 + 1) / kKBlk;
+
+    // Q fragments (B operand of S^T = K Q^T): row c of block rb = token
+    // t0 + 16 rb + c; dims 32cc + 8g.. (remainder: 32 NC32 + 4g..).
+    h8 qa[RB][NC32 > 0 ? NC32 : 1];
+    h4 qr[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int tok = t0 + 16 * rb + c;
+        const bool ok = head_ok && tok < n;
+        const _Float16* qrow =
+            reinterpret_cast<const _Float16*>(p.q) + ((int64_t)(q0 + (ok ? tok : 0)) * p.num_heads + head) * D;
+#pragma unroll
+        for (int cc = 0; cc < NC32; ++cc)
+            qa[rb][cc] = ok ? *reinterpret_cast<const h8*>(qrow + 32 * cc + 8 * g) : h8{};
+        if constexpr (PDims<D>::REM) qr[rb] = ok ? *reinterpret_cast<const h4*>(qrow + 32 * NC32 + 4 * g) : h4{};
+    }
+
+    f4 o[RB][NT + 1];  // + row-sum column block
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int t = 0; t <= NT; ++t) o[rb][t] = f4{0.f, 0.f, 0.f, 0.f};
+    float m_run[RB];  // running max (log2 units) of row c of each block
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) m_run[rb] = kMaxSeed;
+    const h8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+
+    BlockLoader<KV, D> ld;
+    ld.load(p, table, tlen, kvh, 0, kv_end, tid);
+    ld.store(lds, lds + BUF, tid);
+    __syncthreads();
+
+    for (int kb = 0; kb < nblk; ++kb) {
+        lds_char* kbuf = lds + (kb & 1) * 2 * BUF;
+        lds_char* vbuf = kbuf + BUF;
+        if (kb + 1 < nblk) ld.load(p, table, tlen, kvh, (kb + 1) * kKBlk, kv_end, tid);
+
+        const int key0 = kb * kKBlk;
+        // Tiles on a missing or out-of-range page were loaded as zeros and
+        // must be masked like the reference's skipped positions.
+        bool tile_ok[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            const int lb = (key0 + 16 * kt) / p.block_size;
+            const int bid = lb < tlen ? table[lb] : -1;
+            tile_ok[kt] = bid >= 0 && (int64_t)bid < p.num_blocks;
+        }
+        const bool masked = kb >= nfree || !tile_ok[0] || !tile_ok[1];  // uniform
+        // K fragments of the two 16-key tiles (A operand: row = key c).
+        h8 ka[2][NC32 > 0 ? NC32 : 1];
+        h4 kr[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            lds_char* row = kbuf + (16 * kt + c) * KROW;
+#pragma unroll
+            for (int cc = 0; cc < NC32; ++cc)
+                ka[kt][cc] = *reinterpret_cast<__attribute__((address_space(3))) h8*>(row + (32 * cc + 8 * g) * 2);
+            if constexpr (PDims<D>::REM)
+                kr[kt] = *reinterpret_cast<__attribute__((address_space(3))) h4*>(row + (32 * NC32 + 4 * g) * 2);
+        }
+        // V operands: lane (g, c) gets V[key pi(g, j)][16 t + c] with
+        // pi(g, j) = 4g + j (j < 4), 16 + 4g + j - 4 (j >= 4).
+        h8 vb[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const h4 lo = read_tr(vbuf + (4 * g + (c >> 2)) * KROW + (16 * t + 4 * (c & 3)) * 2);
+            const h4 hi = read_tr(vbuf + (16 + 4 * g + (c >> 2)) * KROW + (16 * t + 4 * (c & 3)) * 2);
+            vb[t] = h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            float sc[2][4];
+            float mx = kMaxSeed;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int cc = 0; cc < NC32; ++cc) acc = mfma32(ka[kt][cc], qa[rb][cc], acc);
+                if constexpr (PDims<D>::REM) {
+                    const f4 zero = {0.f, 0.f, 0.f, 0.f};
+                    const f4 acc2 = mfma16(kr[kt], qr[rb], zero);
+                    acc += acc2;
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float x = acc[r];
+                    if (masked) {
+                        const int key = key0 + 16 * kt + 4 * g + r;
+                        const int tok = t0 + 16 * rb + c;
+                        x = (tile_ok[kt] && key <= prefix + tok && key < kv_end) ? x : -__builtin_inff();
+                    }
+                    sc[kt][r] = x;
+                    mx = fmaxf(mx, x);
+                }
+            }
+            mx = fmaxf(mx, shfl_xor(mx, 16));
+            mx = fmaxf(mx, shfl_xor(mx, 32));
+            mx *= p.scale_log2;  // row max in log2 units (scale > 0)
+            // Lazy rescale: move the running max only when it grows by > 2^8.
+            const bool grow = mx > m_run[rb] + kLazy;
+            if (__any(grow)) {
+                const float m_new = grow ? mx : m_run[rb];
+                const float alpha = fast_exp2(m_run[rb] - m_new);
+                m_run[rb] = m_new;
+                // O row 4g + r lives in lane (4g + r) of row c's layout.
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float a = shfl(alpha, 4 * g + r);
+#pragma unroll
+                    for (int t = 0; t <= NT; ++t) o[rb][t][r] *= a;
+                }
+            }
+            const float mneg = -m_run[rb];
+            h8 pa;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    pa[4 * kt + r] = (_Float16)fast_exp2(fmaf(sc[kt][r], p.scale_log2, mneg));
+#pragma unroll
+            for (int t = 0; t < NT; ++t) o[rb][t] = mfma32(pa, vb[t], o[rb][t]);
+            o[rb][NT] = mfma32(pa, ones, o[rb][NT]);
+        }
+
+        if (kb + 1 < nblk) {
+            lds_char* nk = lds + ((kb + 1) & 1) * 2 * BUF;
+            ld.store(nk, nk + BUF, tid);
+        }
+        __syncthreads();
+    }
+
+    if (!head_ok) return;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tok = t0 + 16 * rb + 4 * g + r;
+            if (tok >= n) continue;
+            // o[.][NT] is the row sum of the same fp16 P that weighted V.
+            const float inv = 1.0f / (o[rb][NT][r] + 1e-9f);
+            float* orow = p.out + ((int64_t)(q0 + tok) * p.num_heads + head) * D;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) orow[16 * t + c] = o[rb][t][r] * inv;
+        }
+    }
+}
+
+template <int KV, int D>
+hipError_t launch(const PrefillParams& p, hipStream_t stream) {
+    dim3 grid((p.max_chunk_len + PDims<D>::QT - 1) / PDims<D>::QT, p.num_chunks,
+              p.num_kv_heads * p.head_groups);
+    hipLaunchKernelGGL((prefill_mfma_kernel<KV, D>), grid, dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+int prefill_head_groups(int group) { return (group + kHeadsPerGroup - 1) / kHeadsPerGroup; }
+
+hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream) {
+    if (p.num_chunks == 0 || p.max_chunk_len == 0) return hipSuccess;
+    const bool prof = prof_enabled();
+    if (prof) prof_begin(kKernelPrefill, stream);
+    hipError_t err = hipErrorInvalidValue;
+#define VCPP_PF_D(KVT)                                               \
+    switch (p.head_dim) {                                            \
+        case 64: err = launch<KVT, 64>(p, stream); break;            \
+        case 80: err = launch<KVT, 80>(p, stream); break;            \
+        case 128: err = launch<KVT, 128>(p, stream); break;          \
+        default: return hipErrorInvalidValue;                        \
+    }
+    if (p.kv_dtype == VCPP_KV_F16) {
+        VCPP_PF_D(VCPP_KV_F16)
+    } else {
+        VCPP_PF_D(VCPP_KV_I8)
+    }
+#undef VCPP_PF_D
+    if (err != hipSuccess) return err;
+    if (prof) prof_end(kKernelPrefill, stream);
+    return hipSuccess;
+}
+
+}  // namespace vcpp

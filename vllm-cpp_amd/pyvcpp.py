@@ -27,6 +27,7 @@ EXPORTS = [
     "vcpp_version",
     "vcpp_paged_decode",
     "vcpp_decode_workspace_size",
+    "vcpp_paged_prefill",
     "paged_attention_cuda",
     "vcpp_profile_enable",
     "vcpp_profile_read",
@@ -77,6 +78,9 @@ def lib():
     L.vcpp_paged_decode.restype = ctypes.c_int
     L.vcpp_decode_workspace_size.argtypes = [ctypes.POINTER(KVPages), i32, i32, i32, i32]
     L.vcpp_decode_workspace_size.restype = sz
+    L.vcpp_paged_prefill.argtypes = [ctypes.POINTER(KVPages), vp, vp, vp, i32, vp, vp, i32, i32,
+                                     i32, vp]
+    L.vcpp_paged_prefill.restype = ctypes.c_int
     L.paged_attention_cuda.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32]
     L.paged_attention_cuda.restype = None
     L.vcpp_profile_enable.argtypes = [ctypes.c_int]
@@ -152,3 +156,13 @@ def profile_read(kernel_id):
     n = ctypes.c_int64()
     _check(lib().vcpp_profile_read(kernel_id, ctypes.byref(ms), ctypes.byref(n)))
     return ms.value, n.value
+
+
+def paged_prefill(pages, q, out, block_tables, q_start, prefix_lens, max_chunk_len, num_heads,
+                  stream=None):
+    """vcpp_paged_prefill on device tensors (q fp16, out fp32)."""
+    rc = lib().vcpp_paged_prefill(ctypes.byref(pages), _ptr(q), _ptr(out), _ptr(block_tables),
+                                  block_tables.shape[1], _ptr(q_start), _ptr(prefix_lens),
+                                  prefix_lens.shape[0], max_chunk_len, num_heads, _stream(stream))
+    _check(rc)
+    return out
