@@ -43,6 +43,8 @@ def parse():
                     help="split-K partition size (0 = library default)")
     ap.add_argument("--prefill-steps", type=int, default=20)
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill leg")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the prefill leg (for profiling its kernel)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a device-to-device copy of 1 GiB five times (the known-size "
                          "kernel that rocprofv3 FETCH_SIZE / WRITE_SIZE readings are scaled by)")
@@ -154,7 +156,7 @@ def bench_prefill(torch, pyvcpp, args):
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": F16_MFMA_PEAK_TFS,
                      "unit": "TFLOP/s", "frac": round(achieved / F16_MFMA_PEAK_TFS, 4),
                      "traffic": read_traffic("prefill_mfma_config3_traffic.txt"),
-                     "kernel": "prefill_mfma_kernel<f16,80>",
+                     "kernel": "prefill_dma_kernel<80>",
                      "kernel_avg_us": round(k_s * 1e6, 1)},
     }
 
@@ -230,6 +232,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": x.numel() * 2, "copy_bytes_written": y.numel() * 2,
                           "launches": 5}))
+        return
+    if args.prefill_only:
+        print(json.dumps(bench_prefill(torch, pyvcpp, args)))
         return
 
     w = decode_workload(torch, args.seed)

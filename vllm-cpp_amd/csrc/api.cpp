@@ -274,6 +274,11 @@ int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
         return fail(VCPP_E_INVALID, "num_heads %d is not a positive multiple of num_kv_heads %d",
                     num_heads, kv->num_kv_heads);
     if (num_chunks > 65535) return fail(VCPP_E_UNSUPPORTED, "too many chunks (%d)", num_chunks);
+    // The kernels stage a tile's block table in LDS (64 KiB per workgroup).
+    if (max_blocks_per_seq > 4096 ||
+        vcpp::prefill_lds_bytes(kv->dtype, kv->head_dim, max_blocks_per_seq) > 65536)
+        return fail(VCPP_E_UNSUPPORTED, "prefill block table of %d entries exceeds the LDS budget",
+                    max_blocks_per_seq);
     vcpp::PrefillParams p{};
     p.k = kv->k;
     p.v = kv->v;
@@ -300,6 +305,7 @@ int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
     p.num_chunks = num_chunks;
     p.max_chunk_len = max_chunk_len;
     p.scale_log2 = (1.0f / std::sqrt((float)kv->head_dim)) * 1.4426950408889634f;
+    p.bs_magic = ((1ull << 40) + kv->block_size - 1) / kv->block_size;
     hipError_t e = vcpp::launch_prefill(p, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "prefill launch");
     return VCPP_OK;

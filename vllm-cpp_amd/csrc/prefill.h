@@ -35,9 +35,12 @@ struct PrefillParams {
     int32_t num_chunks;
     int32_t max_chunk_len;
     float scale_log2;  // log2(e) / sqrt(head_dim)
+    uint64_t bs_magic; // ceil(2^40 / block_size): pos / block_size = (pos * bs_magic) >> 40
 };
 
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream);
 int prefill_head_groups(int group);
+// Dynamic LDS bytes of the prefill kernel for a table of max_blocks entries.
+size_t prefill_lds_bytes(int kv_dtype, int head_dim, int max_blocks);
 
 }  // namespace vcpp

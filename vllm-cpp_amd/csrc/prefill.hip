@@ -28,6 +28,8 @@
 #include "prefill.h"
 #include "profile.h"
 
+#include <type_traits>
+
 namespace vcpp {
 
 namespace {
@@ -35,6 +37,8 @@ namespace {
 constexpr int kKBlk = 32;   // keys per block
 constexpr int kHeadsPerGroup = 4;
 constexpr float kLazy = 8.0f;  // log2 of the largest P allowed before rescaling
+// Block-table entries staged per workgroup: keys < 16 * kMaxTablePages per tile.
+constexpr int kMaxTablePages = 4096;
 
 typedef short s4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) char lds_char;
@@ -69,8 +73,9 @@ struct BlockLoader {
     static constexpr int PER = (TOTAL + 255) / 256;
     h8 reg[PER];
 
-    __device__ __forceinline__ void load(const PrefillParams& p, const int32_t* table, int tlen,
-                                         int kvh, int key0, int kv_end, int tid) {
+    __device__ __forceinline__ void load(const PrefillParams& p,
+                                         const __attribute__((address_space(3))) int32_t* table,
+                                         int tlen, int kvh, int key0, int kv_end, int tid) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int ci = tid + 256 * i;
@@ -82,8 +87,8 @@ struct BlockLoader {
                 const int pos = key0 + key;
                 const int lb = pos / p.block_size;
                 if (pos < kv_end && lb < tlen) {
-                    const int bid = table[lb];
-                    if (bid >= 0 && (int64_t)bid < p.num_blocks) {
+                    const int bid = table[lb];  // staged in LDS, validated
+                    if (bid >= 0) {
                         const int slot = pos - lb * p.block_size;
                         const int64_t e = (int64_t)bid * p.block_stride +
                                           ((int64_t)slot * p.num_kv_heads + kvh) * D + ch * 8;
@@ -124,13 +129,16 @@ struct BlockLoader {
 
 template <int KV, int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void prefill_mfma_kernel(PrefillParams p) {
+void prefill_staged_kernel(PrefillParams p) {
     constexpr int NC32 = PDims<D>::NC32, NT = PDims<D>::NT, RB = PDims<D>::RB;
     constexpr int kQTile = PDims<D>::QT;
     constexpr int KROW = PDims<D>::PITCH;     // bytes per LDS row
     constexpr int BUF = kKBlk * KROW;         // bytes of one K (or V) block
     __shared__ __attribute__((aligned(16))) char lds_raw[4 * BUF];  // 2 x (K, V) blocks
+    __shared__ int32_t table_s[kMaxTablePages];                      // validated block ids
     lds_char* lds = reinterpret_cast<lds_char*>((__attribute__((address_space(3))) char*)lds_raw);
+    const __attribute__((address_space(3))) int32_t* tab =
+        (const __attribute__((address_space(3))) int32_t*)table_s;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
@@ -180,15 +188,24 @@ void prefill_mfma_kernel(PrefillParams p) {
     for (int rb = 0; rb < RB; ++rb) m_run[rb] = kMaxSeed;
     const h8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
 
+    // The tile's block ids, validated once: the K/V gathers then cost one
+    // round trip to memory instead of two (table, then page).
+    const int npages = min((kv_end + p.block_size - 1) / p.block_size, tlen);
+    for (int i = tid; i < npages; i += 256) {
+        const int bid = table[i];
+        table_s[i] = (bid >= 0 && (int64_t)bid < p.num_blocks) ? bid : -1;
+    }
+    __syncthreads();
+
     BlockLoader<KV, D> ld;
-    ld.load(p, table, tlen, kvh, 0, kv_end, tid);
+    ld.load(p, tab, npages, kvh, 0, kv_end, tid);
     ld.store(lds, lds + BUF, tid);
     __syncthreads();
 
     for (int kb = 0; kb < nblk; ++kb) {
         lds_char* kbuf = lds + (kb & 1) * 2 * BUF;
         lds_char* vbuf = kbuf + BUF;
-        if (kb + 1 < nblk) ld.load(p, table, tlen, kvh, (kb + 1) * kKBlk, kv_end, tid);
+        if (kb + 1 < nblk) ld.load(p, tab, npages, kvh, (kb + 1) * kKBlk, kv_end, tid);
 
         const int key0 = kb * kKBlk;
         // Tiles on a missing or out-of-range page were loaded as zeros and
@@ -197,8 +214,7 @@ void prefill_mfma_kernel(PrefillParams p) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
             const int lb = (key0 + 16 * kt) / p.block_size;
-            const int bid = lb < tlen ? table[lb] : -1;
-            tile_ok[kt] = bid >= 0 && (int64_t)bid < p.num_blocks;
+            tile_ok[kt] = lb < npages && tab[lb] >= 0;
         }
         const bool masked = kb >= nfree || !tile_ok[0] || !tile_ok[1];  // uniform
         // K fragments of the two 16-key tiles (A operand: row = key c).
@@ -301,17 +317,322 @@ void prefill_mfma_kernel(PrefillParams p) {
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// fp16 pages: direct-to-LDS gathers through a ring of kStages key blocks.
+//
+// LDS layout of one stage: K then V, each [chunk][32 keys] of 16-byte chunks
+// (chunk = 8 consecutive dims); in odd chunks the key index is XORed with 8.
+// That makes the 16 rows of a K fragment read and the 8-byte transposing V
+// reads of 32 lanes fall on distinct banks.  Each wave-wide DMA instruction
+// fills 64 consecutive chunk slots (1 KiB); a lane picks the page address of
+// the slot it fills, or a zero chunk for keys that are past the tile, on a
+// missing page or out of the pool.
+
+__device__ __attribute__((aligned(16))) const uint32_t kZeroChunk[4] = {0, 0, 0, 0};
+
+template <int D>
+struct DmaDims {
+    static constexpr int NCH = D / 8;              // 16-byte chunks per row
+    static constexpr int REGION = kKBlk * NCH;     // chunk slots of K (or V) per stage
+    static constexpr int NINST = 2 * REGION / 64;  // wave DMA instructions per stage
+    static constexpr int PERW = (NINST + 3) / 4;   // per wave (waves < NINST % 4 do one more)
+    static constexpr int STAGE = 2 * REGION * 16;  // bytes
+    static constexpr int STAGES = D <= 80 ? 4 : 3; // ring depth (LDS: 40 / 48 KiB)
+    static_assert((2 * REGION) % 64 == 0, "stage must be whole DMA instructions");
+};
+
+__device__ __forceinline__ int slot_of(int chunk, int key) { return chunk * kKBlk + (key ^ ((chunk & 1) << 3)); }
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// 16 bytes from global memory to LDS (m0 = wave's destination base; lane l
+// writes bytes [16 l, 16 l + 16) after it).
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                 ::"s"(lds_base), "v"(src) : "memory", "m0");
+}
+
+__device__ __forceinline__ float max_over_groups(float x) {
+    // max over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane groups)
+    const uint32_t b = __builtin_bit_cast(uint32_t, x);
+    const auto s32 = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+    x = fmaxf(__builtin_bit_cast(float, s32[0]), __builtin_bit_cast(float, s32[1]));
+    const uint32_t b2 = __builtin_bit_cast(uint32_t, x);
+    const auto s16 = __builtin_amdgcn_permlane16_swap(b2, b2, false, false);
+    return fmaxf(__builtin_bit_cast(float, s16[0]), __builtin_bit_cast(float, s16[1]));
+}
+
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_dma_kernel(PrefillParams p) {
+    using DD = DmaDims<D>;
+    constexpr int kStages = DD::STAGES;
+    constexpr int NC32 = PDims<D>::NC32, NT = PDims<D>::NT, RB = PDims<D>::RB;
+    constexpr int kQTile = PDims<D>::QT;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    lds_char* lds = reinterpret_cast<lds_char*>((__attribute__((address_space(3))) char*)smem);
+    int32_t* table_s = reinterpret_cast<int32_t*>(smem + kStages * DD::STAGE);
+    const uint32_t lds_addr = (uint32_t)(uintptr_t)lds;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int chunk = blockIdx.y;
+    const int q0 = p.q_start[chunk], n = p.q_start[chunk + 1] - q0;
+    const int ntile = (n + kQTile - 1) / kQTile;
+    const int tile = ntile - 1 - (int)blockIdx.x;  // heaviest (latest) tiles first
+    if (tile < 0) return;                          // whole workgroup: before any barrier
+    const int t0 = tile * kQTile;
+    const int prefix = p.prefix_lens[chunk];
+    const int kvh = blockIdx.z / p.head_groups;
+    const int hg = blockIdx.z - kvh * p.head_groups;
+    const int hl = hg * kHeadsPerGroup + wave;
+    const bool head_ok = hl < p.group;
+    const int head = kvh * p.group + (head_ok ? hl : 0);
+    const int32_t* table = p.block_tables + (int64_t)chunk * p.max_blocks;
+    const int kv_end = prefix + min(t0 + kQTile, n);
+    const int nblk = (kv_end + kKBlk - 1) / kKBlk;
+    const int nfree = (prefix + t0 + 1) / kKBlk;  // blocks visible to every row
+
+    // Q fragments (B operand of S^T = K Q^T).
+    h8 qa[RB][NC32 > 0 ? NC32 : 1];
+    h4 qr[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int tok = t0 + 16 * rb + c;
+        const bool ok = head_ok && tok < n;
+        const _Float16* qrow =
+            reinterpret_cast<const _Float16*>(p.q) + ((int64_t)(q0 + (ok ? tok : 0)) * p.num_heads + head) * D;
+#pragma unroll
+        for (int cc = 0; cc < NC32; ++cc)
+            qa[rb][cc] = ok ? *reinterpret_cast<const h8*>(qrow + 32 * cc + 8 * g) : h8{};
+        if constexpr (PDims<D>::REM) qr[rb] = ok ? *reinterpret_cast<const h4*>(qrow + 32 * NC32 + 4 * g) : h4{};
+    }
+    // Stage the tile's block ids (validated) in LDS; note any bad entry.
+    const int npages = min((kv_end + p.block_size - 1) / p.block_size, p.max_blocks);
+    int bad = 0;
+    for (int i = tid; i < npages; i += 256) {
+        const int bid = table[i];
+        const bool ok = bid >= 0 && (int64_t)bid < p.num_blocks;
+        table_s[i] = ok ? bid : -1;
+        bad |= !ok;
+    }
+    const bool any_bad = __syncthreads_or(bad) != 0;
+    // Q (and table) loads complete here, in a wait the compiler sees: the
+    // ring's DMA below is invisible to its counter bookkeeping, which would
+    // otherwise wait for everything at the Q fragments' first use in the loop.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    // Positions covered by the table: keys at or past tab_end are skipped.
+    const int tab_end = npages * p.block_size;
+
+    // DMA lanes.  Instruction j = wave + 4 i fills chunk slots 64 j + lane of
+    // the stage: region (K or V) and chunk pair are uniform per instruction,
+    // and every instruction's lane l carries key (l & 31) ^ 8 (l >> 5) of
+    // chunk 2 (j mod 2R/64) + (l >> 5) -- one page lookup per lane serves all.
+    constexpr int PERW = DD::PERW;
+    const int my_inst = wave < (DD::NINST & 3) || (DD::NINST & 3) == 0 ? PERW : PERW - 1;
+    const int dkey = (lane & 31) ^ ((lane >> 5) << 3);
+    const int64_t row_bytes = (int64_t)p.num_kv_heads * D * 2;
+    const int64_t page_bytes = p.block_stride * 2;
+    const int64_t lane_off = (int64_t)kvh * D * 2 + (lane >> 5) * 16;
+    auto issue = [&](int kb) {  // DMA key block kb into stage kb % kStages
+        const uint32_t sbase = lds_addr + (kb % kStages) * DD::STAGE;
+        const int pos = kb * kKBlk + dkey;
+        int64_t off = -1;
+        if (pos < kv_end && pos < tab_end) {
+            const int lb = (int)(((uint64_t)(uint32_t)pos * p.bs_magic) >> 40);
+            const int bid = table_s[lb];
+            if (bid >= 0) off = bid * page_bytes + (pos - lb * p.block_size) * row_bytes + lane_off;
+        }
+#pragma unroll
+        for (int i = 0; i < PERW; ++i) {
+            if (i < my_inst) {
+                const int j = wave + 4 * i;
+                const int which = j >= DD::REGION / 64;               // uniform
+                const int cp = j - which * (DD::REGION / 64);          // chunk pair
+                const char* base = static_cast<const char*>(which ? p.v : p.k) + cp * 32;
+                const void* src = off >= 0 ? (const void*)(base + off) : (const void*)kZeroChunk;
+                dma16(src, __builtin_amdgcn_readfirstlane(sbase + j * 1024));
+            }
+        }
+    };
+
+    f4 o[RB][NT + 1];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int t = 0; t <= NT; ++t) o[rb][t] = f4{0.f, 0.f, 0.f, 0.f};
+    float m_run[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) m_run[rb] = kMaxSeed;
+    const h8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+
+    // LDS byte offsets of this lane's fragment reads: one base each plus
+    // compile-time offsets.  K row 16 kt + c of chunk 4 cc + g sits in slot
+    // (4 cc + g) 32 + 16 kt + (c ^ 8 (g & 1)); V rows 16 hh + 4 g + c / 4 of
+    // chunk 2 t + (c & 3) / 2 likewise.
+    const int kbase = (32 * g + (c ^ ((g & 1) << 3))) * 16;
+    const int rpar = (4 * NC32 + (g >> 1)) & 1;
+    const int krbase = ((4 * NC32 + (g >> 1)) * 32 + (c ^ (rpar << 3))) * 16 + 8 * (g & 1);
+    const int vpar = (c >> 1) & 1;
+    const int vbase = DD::REGION * 16 + (((c & 3) >> 1) * 32 + ((4 * g + (c >> 2)) ^ (vpar << 3))) * 16 + 8 * (c & 1);
+
+    auto compute = [&](int kb, auto masked_tag) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
+        lds_char* sb = lds + (kb % kStages) * DD::STAGE;
+        const int key0 = kb * kKBlk;
+        h8 ka[2][NC32 > 0 ? NC32 : 1];
+        h4 kr[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int cc = 0; cc < NC32; ++cc)
+                ka[kt][cc] = *reinterpret_cast<__attribute__((address_space(3))) h8*>(sb + kbase + (128 * cc + 16 * kt) * 16);
+            if constexpr (PDims<D>::REM)
+                kr[kt] = *reinterpret_cast<__attribute__((address_space(3))) h4*>(sb + krbase + 16 * kt * 16);
+        }
+        h8 vb[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const h4 lo = read_tr(sb + vbase + 64 * t * 16);
+            const h4 hi = read_tr(sb + vbase + (64 * t + 16) * 16);
+            vb[t] = h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+        bool tile_ok[2] = {true, true};
+        if constexpr (MASKED) {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                const int k16 = key0 + 16 * kt;
+                const int lb = k16 / p.block_size;
+                tile_ok[kt] = k16 < tab_end && table_s[lb] >= 0;
+            }
+        }
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            float sc[2][4];
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int cc = 0; cc < NC32; ++cc) acc = mfma32(ka[kt][cc], qa[rb][cc], acc);
+                if constexpr (PDims<D>::REM) {
+                    const f4 zero = {0.f, 0.f, 0.f, 0.f};
+                    acc += mfma16(kr[kt], qr[rb], zero);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float x = acc[r];
+                    if constexpr (MASKED) {
+                        const int key = key0 + 16 * kt + 4 * g + r;
+                        const int lim = min(prefix + t0 + 16 * rb + c, kv_end - 1);
+                        x = (tile_ok[kt] && key <= lim) ? x : -__builtin_inff();
+                    }
+                    sc[kt][r] = x;
+                }
+            }
+            float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                             fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+            mx = max_over_groups(mx) * p.scale_log2;
+            const bool grow = mx > m_run[rb] + kLazy;
+            if (__builtin_expect(__any(grow), 0)) {
+                const float m_new = grow ? mx : m_run[rb];
+                const float alpha = fast_exp2(m_run[rb] - m_new);
+                m_run[rb] = m_new;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float a = shfl(alpha, 4 * g + r);
+#pragma unroll
+                    for (int t = 0; t <= NT; ++t) o[rb][t][r] *= a;
+                }
+            }
+            const float mneg = -m_run[rb];
+            h8 pa;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    pa[4 * kt + r] = (_Float16)fast_exp2(fmaf(sc[kt][r], p.scale_log2, mneg));
+#pragma unroll
+            for (int t = 0; t < NT; ++t) o[rb][t] = mfma32(pa, vb[t], o[rb][t]);
+            o[rb][NT] = mfma32(pa, ones, o[rb][NT]);
+        }
+    };
+
+    // Ring: blocks kb .. kb + kStages - 2 in flight while block kb is consumed.
+    // Blocks past nblk are issued too (as zero chunks) so that every wave's
+    // vmcnt arithmetic below stays exact.
+#pragma unroll
+    for (int s = 0; s < kStages - 1; ++s) issue(s);
+    const int free_end = any_bad ? 0 : min(nfree, nblk);
+    auto step = [&](int kb) {
+        if (my_inst == PERW) wait_vmcnt<(kStages - 2) * PERW>();
+        else wait_vmcnt<(kStages - 2) * (PERW > 1 ? PERW - 1 : 1)>();
+        __syncthreads();  // block kb landed for all waves; block kb - 1 consumed
+        issue(kb + kStages - 1);
+    };
+    // Two loops, one inlined compute each (one loop with both variants
+    // merges their accumulators and spills).
+    for (int kb = 0; kb < free_end; ++kb) {
+        step(kb);
+        compute(kb, std::false_type{});
+    }
+    for (int kb = free_end; kb < nblk; ++kb) {
+        step(kb);
+        compute(kb, std::true_type{});
+    }
+    wait_vmcnt<0>();
+
+    if (!head_ok) return;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tok = t0 + 16 * rb + 4 * g + r;
+            if (tok >= n) continue;
+            const float inv = 1.0f / (o[rb][NT][r] + 1e-9f);
+            float* orow = p.out + ((int64_t)(q0 + tok) * p.num_heads + head) * D;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) orow[16 * t + c] = o[rb][t][r] * inv;
+        }
+    }
+}
+
+template <int D>
+hipError_t launch_dma(const PrefillParams& p, hipStream_t stream) {
+    dim3 grid((p.max_chunk_len + PDims<D>::QT - 1) / PDims<D>::QT, p.num_chunks,
+              p.num_kv_heads * p.head_groups);
+    const size_t lds = prefill_lds_bytes(VCPP_KV_F16, D, p.max_blocks);
+    hipLaunchKernelGGL((prefill_dma_kernel<D>), grid, dim3(256), lds, stream, p);
+    return hipGetLastError();
+}
+
 template <int KV, int D>
 hipError_t launch(const PrefillParams& p, hipStream_t stream) {
     dim3 grid((p.max_chunk_len + PDims<D>::QT - 1) / PDims<D>::QT, p.num_chunks,
               p.num_kv_heads * p.head_groups);
-    hipLaunchKernelGGL((prefill_mfma_kernel<KV, D>), grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((prefill_staged_kernel<KV, D>), grid, dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 
 }  // namespace
 
 int prefill_head_groups(int group) { return (group + kHeadsPerGroup - 1) / kHeadsPerGroup; }
+
+size_t prefill_lds_bytes(int kv_dtype, int head_dim, int max_blocks) {
+    if (kv_dtype != VCPP_KV_F16) return 0;  // static LDS only
+    size_t ring = 0;
+    switch (head_dim) {
+        case 64: ring = (size_t)DmaDims<64>::STAGES * DmaDims<64>::STAGE; break;
+        case 80: ring = (size_t)DmaDims<80>::STAGES * DmaDims<80>::STAGE; break;
+        case 128: ring = (size_t)DmaDims<128>::STAGES * DmaDims<128>::STAGE; break;
+        default: return 0;
+    }
+    return ring + (size_t)max_blocks * 4;
+}
 
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream) {
     if (p.num_chunks == 0 || p.max_chunk_len == 0) return hipSuccess;
@@ -326,7 +647,12 @@ hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream) {
         default: return hipErrorInvalidValue;                        \
     }
     if (p.kv_dtype == VCPP_KV_F16) {
-        VCPP_PF_D(VCPP_KV_F16)
+        switch (p.head_dim) {
+            case 64: err = launch_dma<64>(p, stream); break;
+            case 80: err = launch_dma<80>(p, stream); break;
+            case 128: err = launch_dma<128>(p, stream); break;
+            default: return hipErrorInvalidValue;
+        }
     } else {
         VCPP_PF_D(VCPP_KV_I8)
     }
