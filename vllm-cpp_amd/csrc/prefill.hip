@@ -337,7 +337,8 @@ struct DmaDims {
     static constexpr int REGION = kKBlk * NCH;     // chunk slots of K (or V) per stage
     static constexpr int NINST = 2 * REGION / 64;  // wave DMA instructions per stage
     static constexpr int PERW = (NINST + 3) / 4;   // per wave (waves < NINST % 4 do one more)
-    static constexpr int STAGE = 2 * REGION * 16;  // bytes
+    static constexpr int ZERO = 2 * REGION * 16;   // offset of a 16-byte zero slot
+    static constexpr int STAGE = ZERO + 16;        // bytes
     static constexpr int STAGES = D <= 80 ? 4 : 3; // ring depth (LDS: 40 / 48 KiB)
     static_assert((2 * REGION) % 64 == 0, "stage must be whole DMA instructions");
 };
@@ -357,6 +358,12 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
                  ::"s"(lds_base), "v"(src) : "memory", "m0");
 }
 
+// IEEE maximum (NaN-propagating): no operand canonicalisation, and gfx950
+// fuses three-input forms into v_maximum3_f32.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float vmax(float a, float b, float c) { return vmax(vmax(a, b), c); }
+__device__ __forceinline__ float vmax3(float a, float b, float c) { return vmax(vmax(a, b), c); }
+
 __device__ __forceinline__ float max_over_groups(float x) {
     // max over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane groups)
     const uint32_t b = __builtin_bit_cast(uint32_t, x);
@@ -372,6 +379,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_dma_kernel(PrefillParams p) {
     using DD = DmaDims<D>;
     constexpr int kStages = DD::STAGES;
+    constexpr int SG = 2;  // row blocks per softmax group
     constexpr int NC32 = PDims<D>::NC32, NT = PDims<D>::NT, RB = PDims<D>::RB;
     constexpr int kQTile = PDims<D>::QT;
     extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -381,15 +389,30 @@ void prefill_dma_kernel(PrefillParams p) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
-    const int chunk = blockIdx.y;
+    // Workgroups are dealt to the 8 XCDs round-robin by linear id; remap so
+    // that each XCD walks a contiguous range of (tile, chunk, head) ids and
+    // its L2 holds the K/V of the few (chunk, kv head) pairs it is serving.
+    int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+    {
+        const int nx = gridDim.x, ny = gridDim.y;
+        const int total = nx * ny * gridDim.z;
+        if ((total & 7) == 0) {
+            const int lin = bx + nx * (by + ny * bz);
+            const int m = (lin & 7) * (total >> 3) + (lin >> 3);
+            bx = m % nx;
+            by = (m / nx) % ny;
+            bz = m / (nx * ny);
+        }
+    }
+    const int chunk = by;
     const int q0 = p.q_start[chunk], n = p.q_start[chunk + 1] - q0;
     const int ntile = (n + kQTile - 1) / kQTile;
-    const int tile = ntile - 1 - (int)blockIdx.x;  // heaviest (latest) tiles first
-    if (tile < 0) return;                          // whole workgroup: before any barrier
+    const int tile = ntile - 1 - bx;  // heaviest (latest) tiles first
+    if (tile < 0) return;             // whole workgroup: before any barrier
     const int t0 = tile * kQTile;
     const int prefix = p.prefix_lens[chunk];
-    const int kvh = blockIdx.z / p.head_groups;
-    const int hg = blockIdx.z - kvh * p.head_groups;
+    const int kvh = bz / p.head_groups;
+    const int hg = bz - kvh * p.head_groups;
     const int hl = hg * kHeadsPerGroup + wave;
     const bool head_ok = hl < p.group;
     const int head = kvh * p.group + (head_ok ? hl : 0);
@@ -400,7 +423,7 @@ void prefill_dma_kernel(PrefillParams p) {
 
     // Q fragments (B operand of S^T = K Q^T).
     h8 qa[RB][NC32 > 0 ? NC32 : 1];
-    h4 qr[RB];
+    h8 qr[RB];  // dims 32 NC32 + 8 g.. for g < 2, zero for g >= 2 (16-dim remainder)
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
         const int tok = t0 + 16 * rb + c;
@@ -410,8 +433,10 @@ void prefill_dma_kernel(PrefillParams p) {
 #pragma unroll
         for (int cc = 0; cc < NC32; ++cc)
             qa[rb][cc] = ok ? *reinterpret_cast<const h8*>(qrow + 32 * cc + 8 * g) : h8{};
-        if constexpr (PDims<D>::REM) qr[rb] = ok ? *reinterpret_cast<const h4*>(qrow + 32 * NC32 + 4 * g) : h4{};
+        if constexpr (PDims<D>::REM)
+            qr[rb] = ok && g < 2 ? *reinterpret_cast<const h8*>(qrow + 32 * NC32 + 8 * g) : h8{};
     }
+    if (tid < kStages) *reinterpret_cast<__attribute__((address_space(3))) h8*>(lds + tid * DD::STAGE + DD::ZERO) = h8{};
     // Stage the tile's block ids (validated) in LDS; note any bad entry.
     const int npages = min((kv_end + p.block_size - 1) / p.block_size, p.max_blocks);
     int bad = 0;
@@ -466,9 +491,13 @@ void prefill_dma_kernel(PrefillParams p) {
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int t = 0; t <= NT; ++t) o[rb][t] = f4{0.f, 0.f, 0.f, 0.f};
-    float m_run[RB];
+    float m_run[RB], thr[RB];  // running max (log2 units); raw score that triggers a rescale
+    const float inv_scale = 1.0f / p.scale_log2;
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) m_run[rb] = kMaxSeed;
+    for (int rb = 0; rb < RB; ++rb) {
+        m_run[rb] = kMaxSeed;
+        thr[rb] = (kMaxSeed + kLazy) * inv_scale;
+    }
     const h8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
 
     // LDS byte offsets of this lane's fragment reads: one base each plus
@@ -476,8 +505,11 @@ void prefill_dma_kernel(PrefillParams p) {
     // (4 cc + g) 32 + 16 kt + (c ^ 8 (g & 1)); V rows 16 hh + 4 g + c / 4 of
     // chunk 2 t + (c & 3) / 2 likewise.
     const int kbase = (32 * g + (c ^ ((g & 1) << 3))) * 16;
-    const int rpar = (4 * NC32 + (g >> 1)) & 1;
-    const int krbase = ((4 * NC32 + (g >> 1)) * 32 + (c ^ (rpar << 3))) * 16 + 8 * (g & 1);
+    // The 16-dim remainder (D = 80) runs as a 16x16x32 MFMA whose upper half
+    // (lanes g >= 2) reads the stage's zero slot.
+    const int rpar = (4 * NC32 + g) & 1;
+    const int krb0 = g < 2 ? ((4 * NC32 + g) * 32 + (c ^ (rpar << 3))) * 16 : DD::ZERO;
+    const int krb1 = g < 2 ? krb0 + 16 * 16 : DD::ZERO;
     const int vpar = (c >> 1) & 1;
     const int vbase = DD::REGION * 16 + (((c & 3) >> 1) * 32 + ((4 * g + (c >> 2)) ^ (vpar << 3))) * 16 + 8 * (c & 1);
 
@@ -486,14 +518,14 @@ void prefill_dma_kernel(PrefillParams p) {
         lds_char* sb = lds + (kb % kStages) * DD::STAGE;
         const int key0 = kb * kKBlk;
         h8 ka[2][NC32 > 0 ? NC32 : 1];
-        h4 kr[2];
+        h8 kr[2];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
             for (int cc = 0; cc < NC32; ++cc)
                 ka[kt][cc] = *reinterpret_cast<__attribute__((address_space(3))) h8*>(sb + kbase + (128 * cc + 16 * kt) * 16);
             if constexpr (PDims<D>::REM)
-                kr[kt] = *reinterpret_cast<__attribute__((address_space(3))) h4*>(sb + krbase + 16 * kt * 16);
+                kr[kt] = *reinterpret_cast<__attribute__((address_space(3))) h8*>(sb + (kt ? krb1 : krb0));
         }
         h8 vb[NT];
 #pragma unroll
@@ -512,53 +544,73 @@ void prefill_dma_kernel(PrefillParams p) {
             }
         }
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-            float sc[2][4];
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
-                f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int cc = 0; cc < NC32; ++cc) acc = mfma32(ka[kt][cc], qa[rb][cc], acc);
-                if constexpr (PDims<D>::REM) {
-                    const f4 zero = {0.f, 0.f, 0.f, 0.f};
-                    acc += mfma16(kr[kt], qr[rb], zero);
-                }
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float x = acc[r];
-                    if constexpr (MASKED) {
-                        const int key = key0 + 16 * kt + 4 * g + r;
-                        const int lim = min(prefix + t0 + 16 * rb + c, kv_end - 1);
-                        x = (tile_ok[kt] && key <= lim) ? x : -__builtin_inff();
+        for (int rb0 = 0; rb0 < RB; rb0 += SG) {
+            // S^T for SG row blocks at a time: one ballot per group decides
+            // whether any row needs its running max moved, and the compiler can
+            // overlap the softmax of one row block with the MFMAs of the other.
+            float sc[SG][2][4];
+            float mx[SG];
+    #pragma unroll
+            for (int i = 0; i < SG; ++i) {
+                const int rb = rb0 + i;
+    #pragma unroll
+                for (int kt = 0; kt < 2; ++kt) {
+                    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    #pragma unroll
+                    for (int cc = 0; cc < NC32; ++cc) acc = mfma32(ka[kt][cc], qa[rb][cc], acc);
+                    if constexpr (PDims<D>::REM) acc = mfma32(kr[kt], qr[rb], acc);
+    #pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        float x = acc[r];
+                        if constexpr (MASKED) {
+                            const int key = key0 + 16 * kt + 4 * g + r;
+                            const int lim = min(prefix + t0 + 16 * rb + c, kv_end - 1);
+                            x = (tile_ok[kt] && key <= lim) ? x : -__builtin_inff();
+                        }
+                        sc[i][kt][r] = x;
                     }
-                    sc[kt][r] = x;
+                }
+                mx[i] = vmax(vmax3(sc[i][0][0], sc[i][0][1], sc[i][0][2]),
+                              vmax3(sc[i][0][3], sc[i][1][0], sc[i][1][1]),
+                              vmax3(sc[i][1][2], sc[i][1][3], sc[i][1][3]));
+            }
+            // Per-lane test against the raw-score threshold; the row max over
+            // the four lane groups is only formed when some lane crossed it.
+            bool cross = false;
+    #pragma unroll
+            for (int i = 0; i < SG; ++i) cross |= mx[i] > thr[rb0 + i];
+            if (__builtin_expect(__any(cross), 0)) {
+    #pragma unroll
+                for (int i = 0; i < SG; ++i) {
+                    const int rb = rb0 + i;
+                    const float mr = max_over_groups(mx[i]) * p.scale_log2;
+                    const bool grow = mr > m_run[rb] + kLazy;  // uniform per row
+                    const float m_new = grow ? mr : m_run[rb];
+                    const float alpha = fast_exp2(m_run[rb] - m_new);
+                    m_run[rb] = m_new;
+                    thr[rb] = (m_new + kLazy) * inv_scale;
+    #pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float a = shfl(alpha, 4 * g + r);
+    #pragma unroll
+                        for (int t = 0; t <= NT; ++t) o[rb][t][r] *= a;
+                    }
                 }
             }
-            float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
-                             fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
-            mx = max_over_groups(mx) * p.scale_log2;
-            const bool grow = mx > m_run[rb] + kLazy;
-            if (__builtin_expect(__any(grow), 0)) {
-                const float m_new = grow ? mx : m_run[rb];
-                const float alpha = fast_exp2(m_run[rb] - m_new);
-                m_run[rb] = m_new;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float a = shfl(alpha, 4 * g + r);
-#pragma unroll
-                    for (int t = 0; t <= NT; ++t) o[rb][t][r] *= a;
-                }
+    #pragma unroll
+            for (int i = 0; i < SG; ++i) {
+                const int rb = rb0 + i;
+                const float mneg = -m_run[rb];
+                h8 pa;
+    #pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+    #pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        pa[4 * kt + r] = (_Float16)fast_exp2(fmaf(sc[i][kt][r], p.scale_log2, mneg));
+    #pragma unroll
+                for (int t = 0; t < NT; ++t) o[rb][t] = mfma32(pa, vb[t], o[rb][t]);
+                o[rb][NT] = mfma32(pa, ones, o[rb][NT]);
             }
-            const float mneg = -m_run[rb];
-            h8 pa;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    pa[4 * kt + r] = (_Float16)fast_exp2(fmaf(sc[kt][r], p.scale_log2, mneg));
-#pragma unroll
-            for (int t = 0; t < NT; ++t) o[rb][t] = mfma32(pa, vb[t], o[rb][t]);
-            o[rb][NT] = mfma32(pa, ones, o[rb][NT]);
         }
     };
 
