@@ -41,16 +41,21 @@ def _run(cmd, verbose):
         print(err, file=sys.stderr)
 
 
-def build(verbose=False):
+def build(verbose=False, out=LIB, defines=()):
+    """Compiles every source and links `out`; `defines` (e.g. "NAME=1") are
+    passed as -D options, for building variants of the kernels side by side."""
     objs = []
-    os.makedirs(os.path.join(HERE, "_build"), exist_ok=True)
+    tag = "" if out == LIB else "_" + os.path.splitext(os.path.basename(out))[0]
+    bdir = os.path.join(HERE, "_build" + tag)
+    os.makedirs(bdir, exist_ok=True)
+    dflags = ["-D" + d for d in defines]
     for src in SOURCES:
-        obj = os.path.join(HERE, "_build", os.path.basename(src) + ".o")
+        obj = os.path.join(bdir, os.path.basename(src) + ".o")
         lang = ["-x", "hip"]
-        _run([HIPCC] + FLAGS + lang + ["-c", os.path.join(HERE, src), "-o", obj], verbose)
+        _run([HIPCC] + FLAGS + dflags + lang + ["-c", os.path.join(HERE, src), "-o", obj], verbose)
         objs.append(obj)
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", LIB] + objs, verbose)
-    return LIB
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", out] + objs, verbose)
+    return out
 
 
 if __name__ == "__main__":

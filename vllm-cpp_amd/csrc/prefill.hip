@@ -35,12 +35,25 @@ namespace vcpp {
 namespace {
 
 constexpr int kKBlk = 32;   // keys per block
+#ifndef VCPP_PF_EXP_ONEPAGE
+#define VCPP_PF_EXP_ONEPAGE 0
+#endif
+#ifndef VCPP_PF_EXP_NOMEM
+#define VCPP_PF_EXP_NOMEM 0
+#endif
+#ifndef VCPP_PF_EXP_NOCOMPUTE
+#define VCPP_PF_EXP_NOCOMPUTE 0
+#endif
+#ifndef VCPP_PF_PIPE
+#define VCPP_PF_PIPE 1
+#endif
 constexpr int kHeadsPerGroup = 4;
 constexpr float kLazy = 8.0f;  // log2 of the largest P allowed before rescaling
 // Block-table entries staged per workgroup: keys < 16 * kMaxTablePages per tile.
 constexpr int kMaxTablePages = 4096;
 
 typedef short s4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) char lds_char;
 
 template <int D>
@@ -338,8 +351,9 @@ struct DmaDims {
     static constexpr int NINST = 2 * REGION / 64;  // wave DMA instructions per stage
     static constexpr int PERW = (NINST + 3) / 4;   // per wave (waves < NINST % 4 do one more)
     static constexpr int ZERO = 2 * REGION * 16;   // offset of a 16-byte zero slot
-    static constexpr int STAGE = ZERO + 16;        // bytes
-    static constexpr int STAGES = D <= 80 ? 4 : 3; // ring depth (LDS: 40 / 48 KiB)
+    static constexpr int ONE = ZERO + 16;          // slot holding fp16 {1, 0, ..., 0}
+    static constexpr int STAGE = ONE + 16;         // bytes
+    static constexpr int STAGES = D <= 80 ? 6 : 4; // ring depth (LDS: <= 64 KiB)
     static_assert((2 * REGION) % 64 == 0, "stage must be whole DMA instructions");
 };
 
@@ -364,14 +378,18 @@ __device__ __forceinline__ float vmax(float a, float b) { return __builtin_eleme
 __device__ __forceinline__ float vmax(float a, float b, float c) { return vmax(vmax(a, b), c); }
 __device__ __forceinline__ float vmax3(float a, float b, float c) { return vmax(vmax(a, b), c); }
 
+// Reductions over the four 16-lane groups (lanes l, l ^ 16, l ^ 32, l ^ 48).
+// Both run off the hot path (rescales, epilogue), so plain lane shuffles do.
+// (hipcc of this ROCm folds the second result of permlane{16,32}_swap with
+// identical operands into the first, so those builtins are not used here.)
+__device__ __forceinline__ float sum_over_groups(float x) {
+    x += shfl_xor(x, 32);
+    return x + shfl_xor(x, 16);
+}
+
 __device__ __forceinline__ float max_over_groups(float x) {
-    // max over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane groups)
-    const uint32_t b = __builtin_bit_cast(uint32_t, x);
-    const auto s32 = __builtin_amdgcn_permlane32_swap(b, b, false, false);
-    x = fmaxf(__builtin_bit_cast(float, s32[0]), __builtin_bit_cast(float, s32[1]));
-    const uint32_t b2 = __builtin_bit_cast(uint32_t, x);
-    const auto s16 = __builtin_amdgcn_permlane16_swap(b2, b2, false, false);
-    return fmaxf(__builtin_bit_cast(float, s16[0]), __builtin_bit_cast(float, s16[1]));
+    x = vmax(x, shfl_xor(x, 32));
+    return vmax(x, shfl_xor(x, 16));
 }
 
 template <int D>
@@ -380,6 +398,10 @@ void prefill_dma_kernel(PrefillParams p) {
     using DD = DmaDims<D>;
     constexpr int kStages = DD::STAGES;
     constexpr int SG = 2;  // row blocks per softmax group
+    // D with a 16-dim remainder carries the running max in the remainder
+    // MFMA's spare k slot (Q side -m, K side 1), and Q is pre-scaled by
+    // log2(e) / sqrt(D): the MFMA then produces the exp2 argument directly.
+    constexpr bool MCOL = PDims<D>::REM != 0;
     constexpr int NC32 = PDims<D>::NC32, NT = PDims<D>::NT, RB = PDims<D>::RB;
     constexpr int kQTile = PDims<D>::QT;
     extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -435,8 +457,20 @@ void prefill_dma_kernel(PrefillParams p) {
             qa[rb][cc] = ok ? *reinterpret_cast<const h8*>(qrow + 32 * cc + 8 * g) : h8{};
         if constexpr (PDims<D>::REM)
             qr[rb] = ok && g < 2 ? *reinterpret_cast<const h8*>(qrow + 32 * NC32 + 8 * g) : h8{};
+        if constexpr (MCOL) {
+#pragma unroll
+            for (int cc = 0; cc < NC32; ++cc)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qa[rb][cc][e] = (_Float16)((float)qa[rb][cc][e] * p.scale_log2);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qr[rb][e] = (_Float16)((float)qr[rb][e] * p.scale_log2);
+        }
     }
-    if (tid < kStages) *reinterpret_cast<__attribute__((address_space(3))) h8*>(lds + tid * DD::STAGE + DD::ZERO) = h8{};
+    if (tid < kStages) {
+        *reinterpret_cast<__attribute__((address_space(3))) h8*>(lds + tid * DD::STAGE + DD::ZERO) = h8{};
+        *reinterpret_cast<__attribute__((address_space(3))) h8*>(lds + tid * DD::STAGE + DD::ONE) =
+            h8{1, 0, 0, 0, 0, 0, 0, 0};
+    }
     // Stage the tile's block ids (validated) in LDS; note any bad entry.
     const int npages = min((kv_end + p.block_size - 1) / p.block_size, p.max_blocks);
     int bad = 0;
@@ -471,7 +505,11 @@ void prefill_dma_kernel(PrefillParams p) {
         if (pos < kv_end && pos < tab_end) {
             const int lb = (int)(((uint64_t)(uint32_t)pos * p.bs_magic) >> 40);
             const int bid = table_s[lb];
+#if VCPP_PF_EXP_ONEPAGE
+            if (bid >= 0) off = (pos - lb * p.block_size) * row_bytes + lane_off;
+#else
             if (bid >= 0) off = bid * page_bytes + (pos - lb * p.block_size) * row_bytes + lane_off;
+#endif
         }
 #pragma unroll
         for (int i = 0; i < PERW; ++i) {
@@ -481,24 +519,32 @@ void prefill_dma_kernel(PrefillParams p) {
                 const int cp = j - which * (DD::REGION / 64);          // chunk pair
                 const char* base = static_cast<const char*>(which ? p.v : p.k) + cp * 32;
                 const void* src = off >= 0 ? (const void*)(base + off) : (const void*)kZeroChunk;
-                dma16(src, __builtin_amdgcn_readfirstlane(sbase + j * 1024));
+                if (!VCPP_PF_EXP_NOMEM) dma16(src, __builtin_amdgcn_readfirstlane(sbase + j * 1024));
             }
         }
     };
 
-    f4 o[RB][NT + 1];
+    f4 o[RB][NT];
+    // Per-lane partial row sums of the fp16 P that weights V (row c, this
+    // lane's keys), summed over the four lane groups at the end.
+    float lsum[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int t = 0; t <= NT; ++t) o[rb][t] = f4{0.f, 0.f, 0.f, 0.f};
-    float m_run[RB], thr[RB];  // running max (log2 units); raw score that triggers a rescale
+        for (int t = 0; t < NT; ++t) o[rb][t] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) lsum[rb] = 0.f;
+    // Running max per row (log2 units) and the per-lane score above which a
+    // rescale is due.  MCOL: scores arrive already shifted by the max, which
+    // starts at 0 with an infinitely low threshold (the first visible score
+    // sets it); otherwise raw scores are compared against (m + 2^8) / scale.
+    float m_run[RB], thr[RB];
     const float inv_scale = 1.0f / p.scale_log2;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-        m_run[rb] = kMaxSeed;
-        thr[rb] = (kMaxSeed + kLazy) * inv_scale;
+        m_run[rb] = MCOL ? 0.f : kMaxSeed;
+        thr[rb] = MCOL ? -__builtin_inff() : (kMaxSeed + kLazy) * inv_scale;
     }
-    const h8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
 
     // LDS byte offsets of this lane's fragment reads: one base each plus
     // compile-time offsets.  K row 16 kt + c of chunk 4 cc + g sits in slot
@@ -508,8 +554,8 @@ void prefill_dma_kernel(PrefillParams p) {
     // The 16-dim remainder (D = 80) runs as a 16x16x32 MFMA whose upper half
     // (lanes g >= 2) reads the stage's zero slot.
     const int rpar = (4 * NC32 + g) & 1;
-    const int krb0 = g < 2 ? ((4 * NC32 + g) * 32 + (c ^ (rpar << 3))) * 16 : DD::ZERO;
-    const int krb1 = g < 2 ? krb0 + 16 * 16 : DD::ZERO;
+    const int krb0 = g < 2 ? ((4 * NC32 + g) * 32 + (c ^ (rpar << 3))) * 16 : (g == 2 ? DD::ONE : DD::ZERO);
+    const int krb1 = g < 2 ? krb0 + 16 * 16 : krb0;
     const int vpar = (c >> 1) & 1;
     const int vbase = DD::REGION * 16 + (((c & 3) >> 1) * 32 + ((4 * g + (c >> 2)) ^ (vpar << 3))) * 16 + 8 * (c & 1);
 
@@ -543,23 +589,21 @@ void prefill_dma_kernel(PrefillParams p) {
                 tile_ok[kt] = k16 < tab_end && table_s[lb] >= 0;
             }
         }
+        // Row blocks go in groups of SG: S^T of a group, one ballot over the
+        // group (does any row need its running max moved?), then exp and P V.
+        // MCOL: the MFMA already yields S scale log2(e) - m (log2 units);
+        // otherwise raw S, scaled and shifted per element.
+        auto s_group = [&](int rb0, float (&sc)[SG][2][4], float (&mx)[SG]) {
 #pragma unroll
-        for (int rb0 = 0; rb0 < RB; rb0 += SG) {
-            // S^T for SG row blocks at a time: one ballot per group decides
-            // whether any row needs its running max moved, and the compiler can
-            // overlap the softmax of one row block with the MFMAs of the other.
-            float sc[SG][2][4];
-            float mx[SG];
-    #pragma unroll
             for (int i = 0; i < SG; ++i) {
                 const int rb = rb0 + i;
-    #pragma unroll
+#pragma unroll
                 for (int kt = 0; kt < 2; ++kt) {
                     f4 acc = {0.f, 0.f, 0.f, 0.f};
-    #pragma unroll
+#pragma unroll
                     for (int cc = 0; cc < NC32; ++cc) acc = mfma32(ka[kt][cc], qa[rb][cc], acc);
                     if constexpr (PDims<D>::REM) acc = mfma32(kr[kt], qr[rb], acc);
-    #pragma unroll
+#pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         float x = acc[r];
                         if constexpr (MASKED) {
@@ -571,81 +615,142 @@ void prefill_dma_kernel(PrefillParams p) {
                     }
                 }
                 mx[i] = vmax(vmax3(sc[i][0][0], sc[i][0][1], sc[i][0][2]),
-                              vmax3(sc[i][0][3], sc[i][1][0], sc[i][1][1]),
-                              vmax3(sc[i][1][2], sc[i][1][3], sc[i][1][3]));
+                             vmax3(sc[i][0][3], sc[i][1][0], sc[i][1][1]),
+                             vmax3(sc[i][1][2], sc[i][1][3], sc[i][1][3]));
             }
-            // Per-lane test against the raw-score threshold; the row max over
-            // the four lane groups is only formed when some lane crossed it.
+        };
+        // Per-lane test against the threshold; the row max over the four
+        // lane groups is only formed when some lane crossed it.
+        auto check_group = [&](int rb0, float (&sc)[SG][2][4], const float (&mx)[SG]) {
             bool cross = false;
-    #pragma unroll
+#pragma unroll
             for (int i = 0; i < SG; ++i) cross |= mx[i] > thr[rb0 + i];
             if (__builtin_expect(__any(cross), 0)) {
-    #pragma unroll
+#pragma unroll
                 for (int i = 0; i < SG; ++i) {
                     const int rb = rb0 + i;
-                    const float mr = max_over_groups(mx[i]) * p.scale_log2;
-                    const bool grow = mr > m_run[rb] + kLazy;  // uniform per row
-                    const float m_new = grow ? mr : m_run[rb];
-                    const float alpha = fast_exp2(m_run[rb] - m_new);
-                    m_run[rb] = m_new;
-                    thr[rb] = (m_new + kLazy) * inv_scale;
-    #pragma unroll
+                    const float mr = max_over_groups(mx[i]);
+                    const bool grow = mr > thr[rb];  // uniform per row
+                    float alpha;
+                    if constexpr (MCOL) {
+                        // New max rounded to fp16 (it travels in the Q column);
+                        // this block's scores move by the exact difference.
+                        const float m_new = grow ? (float)(_Float16)(m_run[rb] + mr) : m_run[rb];
+                        const float delta = m_new - m_run[rb];
+                        alpha = thr[rb] == -__builtin_inff() ? 0.f : fast_exp2(-delta);
+                        m_run[rb] = m_new;
+                        if (g == 2) qr[rb][0] = (_Float16)(-m_new);
+#pragma unroll
+                        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) sc[i][kt][r] -= delta;
+                        if (grow) thr[rb] = kLazy;
+                    } else {
+                        const float ml = mr * p.scale_log2;
+                        const float m_new = grow ? ml : m_run[rb];
+                        alpha = fast_exp2(m_run[rb] - m_new);
+                        m_run[rb] = m_new;
+                        thr[rb] = (m_new + kLazy) * inv_scale;
+                    }
+                    lsum[rb] *= alpha;  // row c: this lane's own
+#pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const float a = shfl(alpha, 4 * g + r);
-    #pragma unroll
-                        for (int t = 0; t <= NT; ++t) o[rb][t][r] *= a;
+#pragma unroll
+                        for (int t = 0; t < NT; ++t) o[rb][t][r] *= a;
                     }
                 }
             }
-    #pragma unroll
-            for (int i = 0; i < SG; ++i) {
-                const int rb = rb0 + i;
-                const float mneg = -m_run[rb];
-                h8 pa;
-    #pragma unroll
+        };
+        auto p_group = [&](int rb0, const float (&sc)[SG][2][4], h8 (&pa)[SG]) {
+#pragma unroll
+            for (int i = 0; i < SG; ++i)
+#pragma unroll
                 for (int kt = 0; kt < 2; ++kt)
-    #pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        pa[4 * kt + r] = (_Float16)fast_exp2(fmaf(sc[i][kt][r], p.scale_log2, mneg));
-    #pragma unroll
-                for (int t = 0; t < NT; ++t) o[rb][t] = mfma32(pa, vb[t], o[rb][t]);
-                o[rb][NT] = mfma32(pa, ones, o[rb][NT]);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if constexpr (MCOL)
+                            pa[i][4 * kt + r] = (_Float16)fast_exp2(sc[i][kt][r]);
+                        else
+                            pa[i][4 * kt + r] =
+                                (_Float16)fast_exp2(fmaf(sc[i][kt][r], p.scale_log2, -m_run[rb0 + i]));
+                    }
+        };
+        auto pv_group = [&](int rb0, const h8 (&pa)[SG]) {
+#pragma unroll
+            for (int i = 0; i < SG; ++i) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) o[rb0 + i][t] = mfma32(pa[i], vb[t], o[rb0 + i][t]);
+#pragma unroll
+                for (int e = 0; e < 8; e += 2)
+                    lsum[rb0 + i] = __builtin_amdgcn_fdot2(h2{pa[i][e], pa[i][e + 1]}, h2{1, 1}, lsum[rb0 + i], false);
             }
+        };
+        // Two-stage software pipeline over the groups: the exp of group j
+        // runs under the S^T MFMAs of group j + 1, and the P V MFMAs of
+        // group j under the max of group j + 1.
+        float sc[2][SG][2][4], mx[2][SG];
+        h8 pa[SG];
+        s_group(0, sc[0], mx[0]);
+        check_group(0, sc[0], mx[0]);
+#pragma unroll
+        for (int j = 0; j < RB / SG; ++j) {
+#if VCPP_PF_PIPE
+            p_group(j * SG, sc[j & 1], pa);
+            if (j + 1 < RB / SG) s_group((j + 1) * SG, sc[(j + 1) & 1], mx[(j + 1) & 1]);
+            pv_group(j * SG, pa);
+            if (j + 1 < RB / SG) check_group((j + 1) * SG, sc[(j + 1) & 1], mx[(j + 1) & 1]);
+#else
+            p_group(j * SG, sc[j & 1], pa);
+            pv_group(j * SG, pa);
+            if (j + 1 < RB / SG) {
+                s_group((j + 1) * SG, sc[(j + 1) & 1], mx[(j + 1) & 1]);
+                check_group((j + 1) * SG, sc[(j + 1) & 1], mx[(j + 1) & 1]);
+            }
+#endif
         }
     };
 
-    // Ring: blocks kb .. kb + kStages - 2 in flight while block kb is consumed.
+    // Ring of kStages 32-key blocks, consumed two per barrier: while blocks
+    // kb, kb + 1 are computed, blocks up to kb + kStages - 1 are in flight.
     // Blocks past nblk are issued too (as zero chunks) so that every wave's
-    // vmcnt arithmetic below stays exact.
+    // vmcnt arithmetic below stays exact, and an odd tail block is paired
+    // with a fully masked one.
+    static_assert(kStages >= 4 && kStages % 2 == 0, "ring holds whole pairs");
 #pragma unroll
-    for (int s = 0; s < kStages - 1; ++s) issue(s);
-    const int free_end = any_bad ? 0 : min(nfree, nblk);
+    for (int s = 0; s < kStages - 2; ++s) issue(s);
+    const int free_end = any_bad ? 0 : (min(nfree, nblk) & ~1);
     auto step = [&](int kb) {
-        if (my_inst == PERW) wait_vmcnt<(kStages - 2) * PERW>();
-        else wait_vmcnt<(kStages - 2) * (PERW > 1 ? PERW - 1 : 1)>();
-        __syncthreads();  // block kb landed for all waves; block kb - 1 consumed
+        constexpr int kAhead = kStages - 4;  // blocks allowed in flight at the wait
+        if (my_inst == PERW) wait_vmcnt<kAhead * PERW>();
+        else wait_vmcnt<kAhead * (PERW - 1)>();
+        __syncthreads();  // blocks kb, kb + 1 landed for all waves; kb - 2, kb - 1 consumed
+        issue(kb + kStages - 2);
         issue(kb + kStages - 1);
     };
     // Two loops, one inlined compute each (one loop with both variants
     // merges their accumulators and spills).
-    for (int kb = 0; kb < free_end; ++kb) {
+    for (int kb = 0; kb < free_end; kb += 2) {
         step(kb);
-        compute(kb, std::false_type{});
+#pragma unroll 1
+        for (int h = 0; h < 2; ++h) if (!VCPP_PF_EXP_NOCOMPUTE) compute(kb + h, std::false_type{});
     }
-    for (int kb = free_end; kb < nblk; ++kb) {
+    for (int kb = free_end; kb < nblk; kb += 2) {
         step(kb);
-        compute(kb, std::true_type{});
+#pragma unroll 1
+        for (int h = 0; h < 2; ++h) if (!VCPP_PF_EXP_NOCOMPUTE) compute(kb + h, std::true_type{});
     }
     wait_vmcnt<0>();
 
     if (!head_ok) return;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
+        const float rowsum = sum_over_groups(lsum[rb]);  // row c
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
+            const float inv = 1.0f / (shfl(rowsum, 4 * g + r) + 1e-9f);
             const int tok = t0 + 16 * rb + 4 * g + r;
             if (tok >= n) continue;
-            const float inv = 1.0f / (o[rb][NT][r] + 1e-9f);
             float* orow = p.out + ((int64_t)(q0 + tok) * p.num_heads + head) * D;
 #pragma unroll
             for (int t = 0; t < NT; ++t) orow[16 * t + c] = o[rb][t][r] * inv;
@@ -658,6 +763,11 @@ hipError_t launch_dma(const PrefillParams& p, hipStream_t stream) {
     dim3 grid((p.max_chunk_len + PDims<D>::QT - 1) / PDims<D>::QT, p.num_chunks,
               p.num_kv_heads * p.head_groups);
     const size_t lds = prefill_lds_bytes(VCPP_KV_F16, D, p.max_blocks);
+    if (lds > 65536) {
+        const hipError_t e = hipFuncSetAttribute((const void*)prefill_dma_kernel<D>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
     hipLaunchKernelGGL((prefill_dma_kernel<D>), grid, dim3(256), lds, stream, p);
     return hipGetLastError();
 }

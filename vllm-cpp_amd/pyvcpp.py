@@ -9,7 +9,8 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libvcpp_attn.so")
+# VCPP_ATTN_LIB selects another build of the library (e.g. a kernel variant).
+LIB_PATH = os.environ.get("VCPP_ATTN_LIB") or os.path.join(HERE, "libvcpp_attn.so")
 
 VCPP_OK = 0
 VCPP_E_INVALID = -1
