@@ -38,23 +38,40 @@ def test_prefill_small(cuda, kind, heads):
     assert_close(got, want, ATOL, RTOL, what="prefill H=%d Hkv=%d kind=%d" % (H, Hkv, kind))
 
 
+@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8])
 @pytest.mark.parametrize("D", [64, 128])
-def test_prefill_head_dims(cuda, D):
+def test_prefill_head_dims(cuda, D, kind):
     prefix, chunk = [7, 100], [90, 33]
-    pool, q16, q32, tables, q_start, pre = make_case(O.ORC_F16, 610 + D, prefix, chunk, 64, 8, D)
+    pool, q16, q32, tables, q_start, pre = make_case(kind, 610 + D, prefix, chunk, 64, 8, D)
     want = O.prefill(pool, q32, tables, q_start, pre, 64)
     got = gpu_prefill(DevPool(pool), q16, tables, q_start, pre, 64)
-    assert_close(got, want, ATOL, RTOL, what="prefill D=%d" % D)
+    assert_close(got, want, ATOL, RTOL, what="prefill D=%d kind=%d" % (D, kind))
 
 
-def test_prefill_skips_invalid_blocks(cuda):
+@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8])
+def test_prefill_skips_invalid_blocks(cuda, kind):
     prefix, chunk = [48, 0], [40, 70]
-    pool, q16, q32, tables, q_start, pre = make_case(O.ORC_F16, 620, prefix, chunk, 64, 8)
+    pool, q16, q32, tables, q_start, pre = make_case(kind, 620, prefix, chunk, 64, 8)
     tables[0, 1] = -1          # a prefix page missing
     tables[1, 2] = 10 ** 6     # an id past the pool
     want = O.prefill(pool, q32, tables, q_start, pre, 64)
     got = gpu_prefill(DevPool(pool), q16, tables, q_start, pre, 64)
-    assert_close(got, want, ATOL, RTOL, what="prefill invalid blocks")
+    assert_close(got, want, ATOL, RTOL, what="prefill invalid blocks kind=%d" % kind)
+
+
+@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8])
+@pytest.mark.parametrize("D", [64, 80, 128])
+def test_prefill_long_prefix(cuda, kind, D):
+    """Prefixes of several hundred 32-key blocks: many trips round the K/V
+    ring, odd block counts (a masked tail block), chunk lengths that are not
+    multiples of the query tile, and scores large enough (std 2) to move the
+    running max many times."""
+    prefix, chunk = [2500, 3001, 0], [70, 33, 129]
+    pool, q16, q32, tables, q_start, pre = make_case(kind, 650 + D + kind, prefix, chunk, 16, 2,
+                                                     D, std=2.0)
+    want = O.prefill(pool, q32, tables, q_start, pre, 16)
+    got = gpu_prefill(DevPool(pool), q16, tables, q_start, pre, 16)
+    assert_close(got, want, ATOL, RTOL, what="long prefix D=%d kind=%d" % (D, kind))
 
 
 def test_prefill_matches_decode_for_single_token_chunks(cuda):

@@ -274,9 +274,8 @@ int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
         return fail(VCPP_E_INVALID, "num_heads %d is not a positive multiple of num_kv_heads %d",
                     num_heads, kv->num_kv_heads);
     if (num_chunks > 65535) return fail(VCPP_E_UNSUPPORTED, "too many chunks (%d)", num_chunks);
-    // The kernels stage a tile's block table in LDS (160 KiB per workgroup).
-    if (max_blocks_per_seq > 4096 ||
-        vcpp::prefill_lds_bytes(kv->dtype, kv->head_dim, max_blocks_per_seq) > 160 * 1024)
+    // The kernel stages a tile's block table in LDS (160 KiB per workgroup).
+    if (vcpp::prefill_lds_bytes(kv->dtype, kv->head_dim, max_blocks_per_seq) > 160 * 1024)
         return fail(VCPP_E_UNSUPPORTED, "prefill block table of %d entries exceeds the LDS budget",
                     max_blocks_per_seq);
     vcpp::PrefillParams p{};

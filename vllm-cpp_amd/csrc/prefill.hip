@@ -35,22 +35,8 @@ namespace vcpp {
 namespace {
 
 constexpr int kKBlk = 32;   // keys per block
-#ifndef VCPP_PF_EXP_ONEPAGE
-#define VCPP_PF_EXP_ONEPAGE 0
-#endif
-#ifndef VCPP_PF_EXP_NOMEM
-#define VCPP_PF_EXP_NOMEM 0
-#endif
-#ifndef VCPP_PF_EXP_NOCOMPUTE
-#define VCPP_PF_EXP_NOCOMPUTE 0
-#endif
-#ifndef VCPP_PF_PIPE
-#define VCPP_PF_PIPE 1
-#endif
 constexpr int kHeadsPerGroup = 4;
 constexpr float kLazy = 8.0f;  // log2 of the largest P allowed before rescaling
-// Block-table entries staged per workgroup: keys < 16 * kMaxTablePages per tile.
-constexpr int kMaxTablePages = 4096;
 
 typedef short s4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -77,260 +63,6 @@ __device__ __forceinline__ h4 read_tr(lds_char* a) {
 
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
 
-// Gathers key block [key0, key0 + 32) of kv head kvh into LDS rows [key][D]
-// (K at kbuf, V at vbuf), zero rows for keys at or past kv_end or on invalid
-// blocks.  Thread t handles 16-byte chunks t, t + 256, ...
-template <int KV, int D>
-struct BlockLoader {
-    static constexpr int TOTAL = 2 * kKBlk * PDims<D>::CHUNKS;  // K then V chunks
-    static constexpr int PER = (TOTAL + 255) / 256;
-    h8 reg[PER];
-
-    __device__ __forceinline__ void load(const PrefillParams& p,
-                                         const __attribute__((address_space(3))) int32_t* table,
-                                         int tlen, int kvh, int key0, int kv_end, int tid) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int ci = tid + 256 * i;
-            h8 x = {};
-            if (ci < TOTAL) {
-                const int which = ci / (kKBlk * PDims<D>::CHUNKS);  // 0 K, 1 V
-                const int r = ci - which * kKBlk * PDims<D>::CHUNKS;
-                const int key = r / PDims<D>::CHUNKS, ch = r - key * PDims<D>::CHUNKS;
-                const int pos = key0 + key;
-                const int lb = pos / p.block_size;
-                if (pos < kv_end && lb < tlen) {
-                    const int bid = table[lb];  // staged in LDS, validated
-                    if (bid >= 0) {
-                        const int slot = pos - lb * p.block_size;
-                        const int64_t e = (int64_t)bid * p.block_stride +
-                                          ((int64_t)slot * p.num_kv_heads + kvh) * D + ch * 8;
-                        if constexpr (KV == VCPP_KV_F16) {
-                            const _Float16* base = static_cast<const _Float16*>(which ? p.v : p.k);
-                            x = *reinterpret_cast<const h8*>(base + e);
-                        } else {
-                            const int8_t* base = static_cast<const int8_t*>(which ? p.v : p.k);
-                            const i2 raw = *reinterpret_cast<const i2*>(base + e);
-                            const uint16_t* sc = which ? p.v_scale : p.k_scale;
-                            const float s = h2f(sc[(int64_t)bid * p.scale_block_stride +
-                                                   (int64_t)kvh * p.block_size + slot]);
-                            const h8 q = i8x8_to_h8((uint32_t)raw.x, (uint32_t)raw.y);
-#pragma unroll
-                            for (int k = 0; k < 8; ++k) x[k] = (_Float16)((float)q[k] * s);
-                        }
-                    }
-                }
-            }
-            reg[i] = x;
-        }
-    }
-
-    __device__ __forceinline__ void store(lds_char* kbuf, lds_char* vbuf, int tid) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int ci = tid + 256 * i;
-            if (ci < TOTAL) {
-                const int which = ci / (kKBlk * PDims<D>::CHUNKS);
-                const int r = ci - which * kKBlk * PDims<D>::CHUNKS;
-                const int key = r / PDims<D>::CHUNKS, ch = r - key * PDims<D>::CHUNKS;
-                lds_char* dst = (which ? vbuf : kbuf) + key * PDims<D>::PITCH + ch * 16;
-                *reinterpret_cast<__attribute__((address_space(3))) h8*>(dst) = reg[i];
-            }
-        }
-    }
-};
-
-template <int KV, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void prefill_staged_kernel(PrefillParams p) {
-    constexpr int NC32 = PDims<D>::NC32, NT = PDims<D>::NT, RB = PDims<D>::RB;
-    constexpr int kQTile = PDims<D>::QT;
-    constexpr int KROW = PDims<D>::PITCH;     // bytes per LDS row
-    constexpr int BUF = kKBlk * KROW;         // bytes of one K (or V) block
-    __shared__ __attribute__((aligned(16))) char lds_raw[4 * BUF];  // 2 x (K, V) blocks
-    __shared__ int32_t table_s[kMaxTablePages];                      // validated block ids
-    lds_char* lds = reinterpret_cast<lds_char*>((__attribute__((address_space(3))) char*)lds_raw);
-    const __attribute__((address_space(3))) int32_t* tab =
-        (const __attribute__((address_space(3))) int32_t*)table_s;
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int g = lane >> 4, c = lane & 15;
-    const int chunk = blockIdx.y;
-    const int q0 = p.q_start[chunk], n = p.q_start[chunk + 1] - q0;
-    const int ntile = (n + kQTile - 1) / kQTile;
-    const int tile = ntile - 1 - (int)blockIdx.x;  // heaviest (latest) tiles first
-    if (tile < 0) return;                          // whole workgroup: before any barrier
-    const int t0 = tile * kQTile;
-    const int prefix = p.prefix_lens[chunk];
-    const int kvh = blockIdx.z / p.head_groups;
-    const int hg = blockIdx.z - kvh * p.head_groups;
-    const int hl = hg * kHeadsPerGroup + wave;  // head within the GQA group
-    const bool head_ok = hl < p.group;
-    const int head = kvh * p.group + (head_ok ? hl : 0);
-    const int32_t* table = p.block_tables + (int64_t)chunk * p.max_blocks;
-    const int tlen = p.max_blocks;
-    // Keys visible to the tile: positions < prefix + min(t0 + 64, n).
-    const int kv_end = prefix + min(t0 + kQTile, n);
-    const int nblk = (kv_end + kKBlk - 1) / kKBlk;
-    // Key blocks wholly visible to every row of the tile need no mask.
-    const int nfree = (prefix + t0 + 1) / kKBlk;
-
-    // Q fragments (B operand of S^T = K Q^T): row c of block rb = token
-    // t0 + 16 rb + c; dims 32cc + 8g.. (remainder: 32 NC32 + 4g..).
-    h8 qa[RB][NC32 > 0 ? NC32 : 1];
-    h4 qr[RB];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-        const int tok = t0 + 16 * rb + c;
-        const bool ok = head_ok && tok < n;
-        const _Float16* qrow =
-            reinterpret_cast<const _Float16*>(p.q) + ((int64_t)(q0 + (ok ? tok : 0)) * p.num_heads + head) * D;
-#pragma unroll
-        for (int cc = 0; cc < NC32; ++cc)
-            qa[rb][cc] = ok ? *reinterpret_cast<const h8*>(qrow + 32 * cc + 8 * g) : h8{};
-        if constexpr (PDims<D>::REM) qr[rb] = ok ? *reinterpret_cast<const h4*>(qrow + 32 * NC32 + 4 * g) : h4{};
-    }
-
-    f4 o[RB][NT + 1];  // + row-sum column block
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-        for (int t = 0; t <= NT; ++t) o[rb][t] = f4{0.f, 0.f, 0.f, 0.f};
-    float m_run[RB];  // running max (log2 units) of row c of each block
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) m_run[rb] = kMaxSeed;
-    const h8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
-
-    // The tile's block ids, validated once: the K/V gathers then cost one
-    // round trip to memory instead of two (table, then page).
-    const int npages = min((kv_end + p.block_size - 1) / p.block_size, tlen);
-    for (int i = tid; i < npages; i += 256) {
-        const int bid = table[i];
-        table_s[i] = (bid >= 0 && (int64_t)bid < p.num_blocks) ? bid : -1;
-    }
-    __syncthreads();
-
-    BlockLoader<KV, D> ld;
-    ld.load(p, tab, npages, kvh, 0, kv_end, tid);
-    ld.store(lds, lds + BUF, tid);
-    __syncthreads();
-
-    for (int kb = 0; kb < nblk; ++kb) {
-        lds_char* kbuf = lds + (kb & 1) * 2 * BUF;
-        lds_char* vbuf = kbuf + BUF;
-        if (kb + 1 < nblk) ld.load(p, tab, npages, kvh, (kb + 1) * kKBlk, kv_end, tid);
-
-        const int key0 = kb * kKBlk;
-        // Tiles on a missing or out-of-range page were loaded as zeros and
-        // must be masked like the reference's skipped positions.
-        bool tile_ok[2];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            const int lb = (key0 + 16 * kt) / p.block_size;
-            tile_ok[kt] = lb < npages && tab[lb] >= 0;
-        }
-        const bool masked = kb >= nfree || !tile_ok[0] || !tile_ok[1];  // uniform
-        // K fragments of the two 16-key tiles (A operand: row = key c).
-        h8 ka[2][NC32 > 0 ? NC32 : 1];
-        h4 kr[2];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            lds_char* row = kbuf + (16 * kt + c) * KROW;
-#pragma unroll
-            for (int cc = 0; cc < NC32; ++cc)
-                ka[kt][cc] = *reinterpret_cast<__attribute__((address_space(3))) h8*>(row + (32 * cc + 8 * g) * 2);
-            if constexpr (PDims<D>::REM)
-                kr[kt] = *reinterpret_cast<__attribute__((address_space(3))) h4*>(row + (32 * NC32 + 4 * g) * 2);
-        }
-        // V operands: lane (g, c) gets V[key pi(g, j)][16 t + c] with
-        // pi(g, j) = 4g + j (j < 4), 16 + 4g + j - 4 (j >= 4).
-        h8 vb[NT];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const h4 lo = read_tr(vbuf + (4 * g + (c >> 2)) * KROW + (16 * t + 4 * (c & 3)) * 2);
-            const h4 hi = read_tr(vbuf + (16 + 4 * g + (c >> 2)) * KROW + (16 * t + 4 * (c & 3)) * 2);
-            vb[t] = h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
-
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-            float sc[2][4];
-            float mx = kMaxSeed;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
-                f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int cc = 0; cc < NC32; ++cc) acc = mfma32(ka[kt][cc], qa[rb][cc], acc);
-                if constexpr (PDims<D>::REM) {
-                    const f4 zero = {0.f, 0.f, 0.f, 0.f};
-                    const f4 acc2 = mfma16(kr[kt], qr[rb], zero);
-                    acc += acc2;
-                }
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float x = acc[r];
-                    if (masked) {
-                        const int key = key0 + 16 * kt + 4 * g + r;
-                        const int tok = t0 + 16 * rb + c;
-                        x = (tile_ok[kt] && key <= prefix + tok && key < kv_end) ? x : -__builtin_inff();
-                    }
-                    sc[kt][r] = x;
-                    mx = fmaxf(mx, x);
-                }
-            }
-            mx = fmaxf(mx, shfl_xor(mx, 16));
-            mx = fmaxf(mx, shfl_xor(mx, 32));
-            mx *= p.scale_log2;  // row max in log2 units (scale > 0)
-            // Lazy rescale: move the running max only when it grows by > 2^8.
-            const bool grow = mx > m_run[rb] + kLazy;
-            if (__any(grow)) {
-                const float m_new = grow ? mx : m_run[rb];
-                const float alpha = fast_exp2(m_run[rb] - m_new);
-                m_run[rb] = m_new;
-                // O row 4g + r lives in lane (4g + r) of row c's layout.
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float a = shfl(alpha, 4 * g + r);
-#pragma unroll
-                    for (int t = 0; t <= NT; ++t) o[rb][t][r] *= a;
-                }
-            }
-            const float mneg = -m_run[rb];
-            h8 pa;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    pa[4 * kt + r] = (_Float16)fast_exp2(fmaf(sc[kt][r], p.scale_log2, mneg));
-#pragma unroll
-            for (int t = 0; t < NT; ++t) o[rb][t] = mfma32(pa, vb[t], o[rb][t]);
-            o[rb][NT] = mfma32(pa, ones, o[rb][NT]);
-        }
-
-        if (kb + 1 < nblk) {
-            lds_char* nk = lds + ((kb + 1) & 1) * 2 * BUF;
-            ld.store(nk, nk + BUF, tid);
-        }
-        __syncthreads();
-    }
-
-    if (!head_ok) return;
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int tok = t0 + 16 * rb + 4 * g + r;
-            if (tok >= n) continue;
-            // o[.][NT] is the row sum of the same fp16 P that weighted V.
-            const float inv = 1.0f / (o[rb][NT][r] + 1e-9f);
-            float* orow = p.out + ((int64_t)(q0 + tok) * p.num_heads + head) * D;
-#pragma unroll
-            for (int t = 0; t < NT; ++t) orow[16 * t + c] = o[rb][t][r] * inv;
-        }
-    }
-}
-
-
 // ---------------------------------------------------------------------------
 // fp16 pages: direct-to-LDS gathers through a ring of kStages key blocks.
 //
@@ -351,13 +83,34 @@ struct DmaDims {
     static constexpr int NINST = 2 * REGION / 64;  // wave DMA instructions per stage
     static constexpr int PERW = (NINST + 3) / 4;   // per wave (waves < NINST % 4 do one more)
     static constexpr int ZERO = 2 * REGION * 16;   // offset of a 16-byte zero slot
-    static constexpr int ONE = ZERO + 16;          // slot holding fp16 {1, 0, ..., 0}
-    static constexpr int STAGE = ONE + 16;         // bytes
+    static constexpr int STAGE = ZERO + 16;        // bytes
     static constexpr int STAGES = D <= 80 ? 6 : 4; // ring depth (LDS: <= 64 KiB)
     static_assert((2 * REGION) % 64 == 0, "stage must be whole DMA instructions");
 };
 
 __device__ __forceinline__ int slot_of(int chunk, int key) { return chunk * kKBlk + (key ^ ((chunk & 1) << 3)); }
+
+// int8 pages: raw K/V chunks ([chunk of 16 dims][32 keys], 16 bytes per
+// slot, K region then V region) and the 32 + 32 fp16 scales of the block (one
+// dword per lane), dequantised by the workgroup into fp16 DmaDims stages.
+template <int D>
+struct I8Dims {
+    static constexpr int NCH = D / 16;             // 16-byte int8 chunks per row
+    static constexpr int REGION = kKBlk * NCH;     // slots of K (or V)
+    static constexpr int NDATA = 2 * REGION / 64;  // data DMA instructions per block
+    static constexpr int NINST = NDATA + 1;        // + one for the scales
+    static constexpr int PERW = (NINST + 3) / 4;
+    static constexpr int SCALES = 2 * REGION * 16; // offset of the scale dwords
+    static constexpr int STAGE = SCALES + 64 * 4;
+    static constexpr int STAGES = D <= 80 ? 8 : 4; // ring depth
+    static constexpr int UNITS = 2 * REGION;       // dequant units (16 dims) per block
+    static_assert((2 * REGION) % 64 == 0, "int8 stage must be whole DMA instructions");
+};
+
+// Query row blocks per wave: 4 (2 for D = 128) with fp16 pages; int8 pages
+// carry per-key scale state and use 2.
+template <int KV, int D>
+constexpr int rows_blocks() { return KV == VCPP_KV_I8 ? 2 : PDims<D>::RB; }
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -367,9 +120,19 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 // 16 bytes from global memory to LDS (m0 = wave's destination base; lane l
 // writes bytes [16 l, 16 l + 16) after it).
+// m0 is saved and restored around the load: the compiler does not honour a
+// clobber of it.
 __device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
-                 ::"s"(lds_base), "v"(src) : "memory", "m0");
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved) : "s"(lds_base), "v"(src) : "memory");
+}
+
+// 2 bytes from global memory to LDS, zero-extended into lane l's dword.
+__device__ __forceinline__ void dma2(const void* src, uint32_t lds_base) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_ushort %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved) : "s"(lds_base), "v"(src) : "memory");
 }
 
 // IEEE maximum (NaN-propagating): no operand canonicalisation, and gfx950
@@ -392,21 +155,26 @@ __device__ __forceinline__ float max_over_groups(float x) {
     return vmax(x, shfl_xor(x, 16));
 }
 
-template <int D>
+template <int KV, int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_dma_kernel(PrefillParams p) {
     using DD = DmaDims<D>;
-    constexpr int kStages = DD::STAGES;
+    using ID = I8Dims<D>;
+    constexpr bool I8 = KV == VCPP_KV_I8;
+    // LDS: the DMA ring (fp16 stages, or int8 stages plus an fp16 area of two
+    // dequantised blocks), then the tile's block table.
+    constexpr int kStages = I8 ? ID::STAGES : DD::STAGES;
+    constexpr int RSTAGE = I8 ? ID::STAGE : DD::STAGE;
+    constexpr int AREA = kStages * RSTAGE;
+    constexpr int NF16 = I8 ? 2 : kStages;       // fp16-format stages
+    constexpr int F16BASE = I8 ? AREA : 0;
     constexpr int SG = 2;  // row blocks per softmax group
-    // D with a 16-dim remainder carries the running max in the remainder
-    // MFMA's spare k slot (Q side -m, K side 1), and Q is pre-scaled by
-    // log2(e) / sqrt(D): the MFMA then produces the exp2 argument directly.
-    constexpr bool MCOL = PDims<D>::REM != 0;
-    constexpr int NC32 = PDims<D>::NC32, NT = PDims<D>::NT, RB = PDims<D>::RB;
-    constexpr int kQTile = PDims<D>::QT;
+    constexpr int NC32 = PDims<D>::NC32, NT = PDims<D>::NT;
+    constexpr int RB = rows_blocks<KV, D>();  // 16-row blocks per wave
+    constexpr int kQTile = 16 * RB;
     extern __shared__ __attribute__((aligned(16))) char smem[];
     lds_char* lds = reinterpret_cast<lds_char*>((__attribute__((address_space(3))) char*)smem);
-    int32_t* table_s = reinterpret_cast<int32_t*>(smem + kStages * DD::STAGE);
+    int32_t* table_s = reinterpret_cast<int32_t*>(smem + AREA + (I8 ? 2 * DD::STAGE : 0));
     const uint32_t lds_addr = (uint32_t)(uintptr_t)lds;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -457,19 +225,9 @@ void prefill_dma_kernel(PrefillParams p) {
             qa[rb][cc] = ok ? *reinterpret_cast<const h8*>(qrow + 32 * cc + 8 * g) : h8{};
         if constexpr (PDims<D>::REM)
             qr[rb] = ok && g < 2 ? *reinterpret_cast<const h8*>(qrow + 32 * NC32 + 8 * g) : h8{};
-        if constexpr (MCOL) {
-#pragma unroll
-            for (int cc = 0; cc < NC32; ++cc)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) qa[rb][cc][e] = (_Float16)((float)qa[rb][cc][e] * p.scale_log2);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qr[rb][e] = (_Float16)((float)qr[rb][e] * p.scale_log2);
-        }
     }
-    if (tid < kStages) {
-        *reinterpret_cast<__attribute__((address_space(3))) h8*>(lds + tid * DD::STAGE + DD::ZERO) = h8{};
-        *reinterpret_cast<__attribute__((address_space(3))) h8*>(lds + tid * DD::STAGE + DD::ONE) =
-            h8{1, 0, 0, 0, 0, 0, 0, 0};
+    if (tid < NF16) {
+        *reinterpret_cast<__attribute__((address_space(3))) h8*>(lds + F16BASE + tid * DD::STAGE + DD::ZERO) = h8{};
     }
     // Stage the tile's block ids (validated) in LDS; note any bad entry.
     const int npages = min((kv_end + p.block_size - 1) / p.block_size, p.max_blocks);
@@ -505,11 +263,7 @@ void prefill_dma_kernel(PrefillParams p) {
         if (pos < kv_end && pos < tab_end) {
             const int lb = (int)(((uint64_t)(uint32_t)pos * p.bs_magic) >> 40);
             const int bid = table_s[lb];
-#if VCPP_PF_EXP_ONEPAGE
-            if (bid >= 0) off = (pos - lb * p.block_size) * row_bytes + lane_off;
-#else
             if (bid >= 0) off = bid * page_bytes + (pos - lb * p.block_size) * row_bytes + lane_off;
-#endif
         }
 #pragma unroll
         for (int i = 0; i < PERW; ++i) {
@@ -519,7 +273,68 @@ void prefill_dma_kernel(PrefillParams p) {
                 const int cp = j - which * (DD::REGION / 64);          // chunk pair
                 const char* base = static_cast<const char*>(which ? p.v : p.k) + cp * 32;
                 const void* src = off >= 0 ? (const void*)(base + off) : (const void*)kZeroChunk;
-                if (!VCPP_PF_EXP_NOMEM) dma16(src, __builtin_amdgcn_readfirstlane(sbase + j * 1024));
+                dma16(src, __builtin_amdgcn_readfirstlane(sbase + j * 1024));
+            }
+        }
+    };
+
+    // int8: instruction j = wave + 4 i (j < NDATA) fills slots 64 j + lane,
+    // whose key is lane & 31 for every j; the last instruction brings the
+    // scales (lanes 0-31 K, 32-63 V).
+    constexpr int PERW8 = ID::PERW;
+    const int my_inst8 = (ID::NINST & 3) == 0 || wave < (ID::NINST & 3) ? PERW8 : PERW8 - 1;
+    auto issue8 = [&](int kb) {
+        const uint32_t sbase = lds_addr + (kb % kStages) * RSTAGE;
+        const int key = lane & 31;
+        const int pos = kb * kKBlk + key;
+        int64_t off = -1, soff = 0;
+        if (pos < kv_end && pos < tab_end) {
+            const int lb = (int)(((uint64_t)(uint32_t)pos * p.bs_magic) >> 40);
+            const int bid = table_s[lb];
+            if (bid >= 0) {
+                const int slot = pos - lb * p.block_size;
+                off = bid * p.block_stride + ((int64_t)slot * p.num_kv_heads + kvh) * D;
+                soff = ((int64_t)bid * p.scale_block_stride + (int64_t)kvh * p.block_size + slot) * 2;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < PERW8; ++i) {
+            if (i < my_inst8) {
+                const int j = wave + 4 * i;
+                if (j < ID::NDATA) {
+                    const int sl = 64 * j + lane;
+                    const int which = sl >= ID::REGION;
+                    const int ch = (sl - which * ID::REGION) >> 5;
+                    const char* base = static_cast<const char*>(which ? p.v : p.k) + ch * 16;
+                    dma16(off >= 0 ? (const void*)(base + off) : (const void*)kZeroChunk,
+                          __builtin_amdgcn_readfirstlane(sbase + j * 1024));
+                } else {
+                    const char* base = reinterpret_cast<const char*>(lane >> 5 ? p.v_scale : p.k_scale);
+                    dma2(off >= 0 ? (const void*)(base + soff) : (const void*)kZeroChunk,
+                         __builtin_amdgcn_readfirstlane(sbase + ID::SCALES));
+                }
+            }
+        }
+    };
+    // Blocks kb, kb + 1 (int8 ring) -> the fp16 area as exact fp16 integers;
+    // the per-key scales are applied in fp32 to the scores (K) and to P (V).
+    auto widen = [&](int kb) {
+#pragma unroll
+        for (int u0 = 0; u0 < 2 * ID::UNITS; u0 += 256) {
+            const int u = u0 + tid;
+            if (u < 2 * ID::UNITS) {
+                const int blk = u >= ID::UNITS;
+                const int v = u - blk * ID::UNITS;
+                const int which = v >= ID::REGION;
+                const int q = v - which * ID::REGION;
+                const int ch = q >> 5, key = q & 31;
+                lds_char* st = lds + ((kb + blk) % kStages) * RSTAGE;
+                const i4 raw = *reinterpret_cast<__attribute__((address_space(3))) i4*>(st + v * 16);
+                const h8 lo = i8x8_to_h8((uint32_t)raw.x, (uint32_t)raw.y);
+                const h8 hi = i8x8_to_h8((uint32_t)raw.z, (uint32_t)raw.w);
+                lds_char* dst = lds + AREA + blk * DD::STAGE + which * DD::REGION * 16;
+                *reinterpret_cast<__attribute__((address_space(3))) h8*>(dst + slot_of(2 * ch, key) * 16) = lo;
+                *reinterpret_cast<__attribute__((address_space(3))) h8*>(dst + slot_of(2 * ch + 1, key) * 16) = hi;
             }
         }
     };
@@ -535,15 +350,14 @@ void prefill_dma_kernel(PrefillParams p) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) lsum[rb] = 0.f;
     // Running max per row (log2 units) and the per-lane score above which a
-    // rescale is due.  MCOL: scores arrive already shifted by the max, which
-    // starts at 0 with an infinitely low threshold (the first visible score
-    // sets it); otherwise raw scores are compared against (m + 2^8) / scale.
+    // rescale is due: raw scores against (m + 2^8) / scale (fp16 pages), or
+    // already scaled scores (int8 pages) against m + 2^8.
     float m_run[RB], thr[RB];
     const float inv_scale = 1.0f / p.scale_log2;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-        m_run[rb] = MCOL ? 0.f : kMaxSeed;
-        thr[rb] = MCOL ? -__builtin_inff() : (kMaxSeed + kLazy) * inv_scale;
+        m_run[rb] = kMaxSeed;
+        thr[rb] = I8 ? kMaxSeed + kLazy : (kMaxSeed + kLazy) * inv_scale;
     }
 
     // LDS byte offsets of this lane's fragment reads: one base each plus
@@ -552,16 +366,16 @@ void prefill_dma_kernel(PrefillParams p) {
     // chunk 2 t + (c & 3) / 2 likewise.
     const int kbase = (32 * g + (c ^ ((g & 1) << 3))) * 16;
     // The 16-dim remainder (D = 80) runs as a 16x16x32 MFMA whose upper half
-    // (lanes g >= 2) reads the stage's zero slot.
+    // (lanes g >= 2) reads the stage's zero slot (Q side zero too).
     const int rpar = (4 * NC32 + g) & 1;
-    const int krb0 = g < 2 ? ((4 * NC32 + g) * 32 + (c ^ (rpar << 3))) * 16 : (g == 2 ? DD::ONE : DD::ZERO);
+    const int krb0 = g < 2 ? ((4 * NC32 + g) * 32 + (c ^ (rpar << 3))) * 16 : DD::ZERO;
     const int krb1 = g < 2 ? krb0 + 16 * 16 : krb0;
     const int vpar = (c >> 1) & 1;
     const int vbase = DD::REGION * 16 + (((c & 3) >> 1) * 32 + ((4 * g + (c >> 2)) ^ (vpar << 3))) * 16 + 8 * (c & 1);
 
     auto compute = [&](int kb, auto masked_tag) {
         constexpr bool MASKED = decltype(masked_tag)::value;
-        lds_char* sb = lds + (kb % kStages) * DD::STAGE;
+        lds_char* sb = I8 ? lds + AREA + (kb & 1) * DD::STAGE : lds + (kb % kStages) * DD::STAGE;
         const int key0 = kb * kKBlk;
         h8 ka[2][NC32 > 0 ? NC32 : 1];
         h8 kr[2];
@@ -580,6 +394,17 @@ void prefill_dma_kernel(PrefillParams p) {
             const h4 hi = read_tr(sb + vbase + (64 * t + 16) * 16);
             vb[t] = h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
+        // int8: per-key scales of this lane's keys 16 kt + 4 g + r (K's at
+        // which = 0, V's at which = 1), read where they are used.
+        auto scales = [&](int which, float (&sv)[2][4]) {
+            lds_char* scl = lds + (kb % kStages) * RSTAGE + ID::SCALES + which * 32 * 4;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                const i4 w = *reinterpret_cast<__attribute__((address_space(3))) i4*>(scl + (16 * kt + 4 * g) * 4);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sv[kt][r] = (float)__builtin_bit_cast(_Float16, (uint16_t)w[r]);
+            }
+        };
         bool tile_ok[2] = {true, true};
         if constexpr (MASKED) {
 #pragma unroll
@@ -591,9 +416,17 @@ void prefill_dma_kernel(PrefillParams p) {
         }
         // Row blocks go in groups of SG: S^T of a group, one ballot over the
         // group (does any row need its running max moved?), then exp and P V.
-        // MCOL: the MFMA already yields S scale log2(e) - m (log2 units);
-        // otherwise raw S, scaled and shifted per element.
+        // fp16 pages: raw S, scaled and shifted per element in one fma;
+        // int8 pages: S times the key's scale (log2 units).
         auto s_group = [&](int rb0, float (&sc)[SG][2][4], float (&mx)[SG]) {
+            float ks[2][4];  // int8: K scales times log2(e) / sqrt(D)
+            if constexpr (I8) {
+                scales(0, ks);
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) ks[kt][r] *= p.scale_log2;
+            }
 #pragma unroll
             for (int i = 0; i < SG; ++i) {
                 const int rb = rb0 + i;
@@ -606,6 +439,7 @@ void prefill_dma_kernel(PrefillParams p) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         float x = acc[r];
+                        if constexpr (I8) x *= ks[kt][r];
                         if constexpr (MASKED) {
                             const int key = key0 + 16 * kt + 4 * g + r;
                             const int lim = min(prefix + t0 + 16 * rb + c, kv_end - 1);
@@ -632,19 +466,11 @@ void prefill_dma_kernel(PrefillParams p) {
                     const float mr = max_over_groups(mx[i]);
                     const bool grow = mr > thr[rb];  // uniform per row
                     float alpha;
-                    if constexpr (MCOL) {
-                        // New max rounded to fp16 (it travels in the Q column);
-                        // this block's scores move by the exact difference.
-                        const float m_new = grow ? (float)(_Float16)(m_run[rb] + mr) : m_run[rb];
-                        const float delta = m_new - m_run[rb];
-                        alpha = thr[rb] == -__builtin_inff() ? 0.f : fast_exp2(-delta);
+                    if constexpr (I8) {
+                        const float m_new = grow ? mr : m_run[rb];
+                        alpha = fast_exp2(m_run[rb] - m_new);
                         m_run[rb] = m_new;
-                        if (g == 2) qr[rb][0] = (_Float16)(-m_new);
-#pragma unroll
-                        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) sc[i][kt][r] -= delta;
-                        if (grow) thr[rb] = kLazy;
+                        thr[rb] = m_new + kLazy;
                     } else {
                         const float ml = mr * p.scale_log2;
                         const float m_new = grow ? ml : m_run[rb];
@@ -663,15 +489,21 @@ void prefill_dma_kernel(PrefillParams p) {
             }
         };
         auto p_group = [&](int rb0, const float (&sc)[SG][2][4], h8 (&pa)[SG]) {
+            float vs[2][4];  // int8: V scales
+            if constexpr (I8) scales(1, vs);
 #pragma unroll
             for (int i = 0; i < SG; ++i)
 #pragma unroll
                 for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        if constexpr (MCOL)
-                            pa[i][4 * kt + r] = (_Float16)fast_exp2(sc[i][kt][r]);
-                        else
+                        if constexpr (I8) {
+                            // P (fp32) into the row sum; P times the V scale,
+                            // rounded once, weights the int8 V values.
+                            const float pr = fast_exp2(sc[i][kt][r] - m_run[rb0 + i]);
+                            lsum[rb0 + i] += pr;
+                            pa[i][4 * kt + r] = (_Float16)(pr * vs[kt][r]);
+                        } else
                             pa[i][4 * kt + r] =
                                 (_Float16)fast_exp2(fmaf(sc[i][kt][r], p.scale_log2, -m_run[rb0 + i]));
                     }
@@ -681,33 +513,35 @@ void prefill_dma_kernel(PrefillParams p) {
             for (int i = 0; i < SG; ++i) {
 #pragma unroll
                 for (int t = 0; t < NT; ++t) o[rb0 + i][t] = mfma32(pa[i], vb[t], o[rb0 + i][t]);
+                if constexpr (!I8) {  // row sums of exactly the fp16 P that weights V
 #pragma unroll
-                for (int e = 0; e < 8; e += 2)
-                    lsum[rb0 + i] = __builtin_amdgcn_fdot2(h2{pa[i][e], pa[i][e + 1]}, h2{1, 1}, lsum[rb0 + i], false);
+                    for (int e = 0; e < 8; e += 2)
+                        lsum[rb0 + i] =
+                            __builtin_amdgcn_fdot2(h2{pa[i][e], pa[i][e + 1]}, h2{1, 1}, lsum[rb0 + i], false);
+                }
             }
         };
-        // Two-stage software pipeline over the groups: the exp of group j
-        // runs under the S^T MFMAs of group j + 1, and the P V MFMAs of
-        // group j under the max of group j + 1.
+        // fp16: two-stage software pipeline over the groups -- the exp of
+        // group j runs under the S^T MFMAs of group j + 1, and the P V MFMAs
+        // of group j under the max of group j + 1.  int8 (more live scale
+        // state) takes the groups one after the other.
         float sc[2][SG][2][4], mx[2][SG];
         h8 pa[SG];
         s_group(0, sc[0], mx[0]);
         check_group(0, sc[0], mx[0]);
 #pragma unroll
         for (int j = 0; j < RB / SG; ++j) {
-#if VCPP_PF_PIPE
+            const bool more = j + 1 < RB / SG;
+            const int nx = (j + 1) & 1;
             p_group(j * SG, sc[j & 1], pa);
-            if (j + 1 < RB / SG) s_group((j + 1) * SG, sc[(j + 1) & 1], mx[(j + 1) & 1]);
-            pv_group(j * SG, pa);
-            if (j + 1 < RB / SG) check_group((j + 1) * SG, sc[(j + 1) & 1], mx[(j + 1) & 1]);
-#else
-            p_group(j * SG, sc[j & 1], pa);
-            pv_group(j * SG, pa);
-            if (j + 1 < RB / SG) {
-                s_group((j + 1) * SG, sc[(j + 1) & 1], mx[(j + 1) & 1]);
-                check_group((j + 1) * SG, sc[(j + 1) & 1], mx[(j + 1) & 1]);
+            if constexpr (!I8) {
+                if (more) s_group((j + 1) * SG, sc[nx], mx[nx]);
+                pv_group(j * SG, pa);
+            } else {
+                pv_group(j * SG, pa);
+                if (more) s_group((j + 1) * SG, sc[nx], mx[nx]);
             }
-#endif
+            if (more) check_group((j + 1) * SG, sc[nx], mx[nx]);
         }
     };
 
@@ -717,28 +551,43 @@ void prefill_dma_kernel(PrefillParams p) {
     // vmcnt arithmetic below stays exact, and an odd tail block is paired
     // with a fully masked one.
     static_assert(kStages >= 4 && kStages % 2 == 0, "ring holds whole pairs");
+    if constexpr (I8) {
 #pragma unroll
-    for (int s = 0; s < kStages - 2; ++s) issue(s);
+        for (int s = 0; s < kStages - 2; ++s) issue8(s);
+    } else {
+#pragma unroll
+        for (int s = 0; s < kStages - 2; ++s) issue(s);
+    }
     const int free_end = any_bad ? 0 : (min(nfree, nblk) & ~1);
     auto step = [&](int kb) {
         constexpr int kAhead = kStages - 4;  // blocks allowed in flight at the wait
-        if (my_inst == PERW) wait_vmcnt<kAhead * PERW>();
-        else wait_vmcnt<kAhead * (PERW - 1)>();
-        __syncthreads();  // blocks kb, kb + 1 landed for all waves; kb - 2, kb - 1 consumed
-        issue(kb + kStages - 2);
-        issue(kb + kStages - 1);
+        if constexpr (I8) {
+            if (my_inst8 == PERW8) wait_vmcnt<kAhead * PERW8>();
+            else wait_vmcnt<kAhead * (PERW8 - 1)>();
+            __syncthreads();  // blocks kb, kb + 1 landed; the fp16 area is free again
+            issue8(kb + kStages - 2);
+            issue8(kb + kStages - 1);
+            widen(kb);
+            __syncthreads();  // fp16 area holds blocks kb, kb + 1
+        } else {
+            if (my_inst == PERW) wait_vmcnt<kAhead * PERW>();
+            else wait_vmcnt<kAhead * (PERW - 1)>();
+            __syncthreads();  // blocks kb, kb + 1 landed for all waves; kb - 2, kb - 1 consumed
+            issue(kb + kStages - 2);
+            issue(kb + kStages - 1);
+        }
     };
     // Two loops, one inlined compute each (one loop with both variants
     // merges their accumulators and spills).
     for (int kb = 0; kb < free_end; kb += 2) {
         step(kb);
 #pragma unroll 1
-        for (int h = 0; h < 2; ++h) if (!VCPP_PF_EXP_NOCOMPUTE) compute(kb + h, std::false_type{});
+        for (int h = 0; h < 2; ++h) compute(kb + h, std::false_type{});
     }
     for (int kb = free_end; kb < nblk; kb += 2) {
         step(kb);
 #pragma unroll 1
-        for (int h = 0; h < 2; ++h) if (!VCPP_PF_EXP_NOCOMPUTE) compute(kb + h, std::true_type{});
+        for (int h = 0; h < 2; ++h) compute(kb + h, std::true_type{});
     }
     wait_vmcnt<0>();
 
@@ -758,42 +607,41 @@ void prefill_dma_kernel(PrefillParams p) {
     }
 }
 
-template <int D>
+template <int KV, int D>
 hipError_t launch_dma(const PrefillParams& p, hipStream_t stream) {
-    dim3 grid((p.max_chunk_len + PDims<D>::QT - 1) / PDims<D>::QT, p.num_chunks,
+    constexpr int QT = 16 * rows_blocks<KV, D>();
+    dim3 grid((p.max_chunk_len + QT - 1) / QT, p.num_chunks,
               p.num_kv_heads * p.head_groups);
-    const size_t lds = prefill_lds_bytes(VCPP_KV_F16, D, p.max_blocks);
+    const size_t lds = prefill_lds_bytes(KV, D, p.max_blocks);
     if (lds > 65536) {
-        const hipError_t e = hipFuncSetAttribute((const void*)prefill_dma_kernel<D>,
+        const hipError_t e = hipFuncSetAttribute((const void*)prefill_dma_kernel<KV, D>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((prefill_dma_kernel<D>), grid, dim3(256), lds, stream, p);
+    hipLaunchKernelGGL((prefill_dma_kernel<KV, D>), grid, dim3(256), lds, stream, p);
     return hipGetLastError();
 }
 
-template <int KV, int D>
-hipError_t launch(const PrefillParams& p, hipStream_t stream) {
-    dim3 grid((p.max_chunk_len + PDims<D>::QT - 1) / PDims<D>::QT, p.num_chunks,
-              p.num_kv_heads * p.head_groups);
-    hipLaunchKernelGGL((prefill_staged_kernel<KV, D>), grid, dim3(256), 0, stream, p);
-    return hipGetLastError();
-}
 
 }  // namespace
 
 int prefill_head_groups(int group) { return (group + kHeadsPerGroup - 1) / kHeadsPerGroup; }
 
 size_t prefill_lds_bytes(int kv_dtype, int head_dim, int max_blocks) {
-    if (kv_dtype != VCPP_KV_F16) return 0;  // static LDS only
-    size_t ring = 0;
+    auto ring = [&](auto d) -> size_t {
+        constexpr int D = decltype(d)::value;
+        if (kv_dtype == VCPP_KV_I8)
+            return (size_t)I8Dims<D>::STAGES * I8Dims<D>::STAGE + 2 * (size_t)DmaDims<D>::STAGE;
+        return (size_t)DmaDims<D>::STAGES * DmaDims<D>::STAGE;
+    };
+    size_t r = 0;
     switch (head_dim) {
-        case 64: ring = (size_t)DmaDims<64>::STAGES * DmaDims<64>::STAGE; break;
-        case 80: ring = (size_t)DmaDims<80>::STAGES * DmaDims<80>::STAGE; break;
-        case 128: ring = (size_t)DmaDims<128>::STAGES * DmaDims<128>::STAGE; break;
+        case 64: r = ring(std::integral_constant<int, 64>{}); break;
+        case 80: r = ring(std::integral_constant<int, 80>{}); break;
+        case 128: r = ring(std::integral_constant<int, 128>{}); break;
         default: return 0;
     }
-    return ring + (size_t)max_blocks * 4;
+    return r + (size_t)max_blocks * 4;
 }
 
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream) {
@@ -801,20 +649,15 @@ hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream) {
     const bool prof = prof_enabled();
     if (prof) prof_begin(kKernelPrefill, stream);
     hipError_t err = hipErrorInvalidValue;
-#define VCPP_PF_D(KVT)                                               \
-    switch (p.head_dim) {                                            \
-        case 64: err = launch<KVT, 64>(p, stream); break;            \
-        case 80: err = launch<KVT, 80>(p, stream); break;            \
-        case 128: err = launch<KVT, 128>(p, stream); break;          \
-        default: return hipErrorInvalidValue;                        \
+#define VCPP_PF_D(KVT)                                      \
+    switch (p.head_dim) {                                   \
+        case 64: err = launch_dma<KVT, 64>(p, stream); break;   \
+        case 80: err = launch_dma<KVT, 80>(p, stream); break;   \
+        case 128: err = launch_dma<KVT, 128>(p, stream); break; \
+        default: return hipErrorInvalidValue;               \
     }
     if (p.kv_dtype == VCPP_KV_F16) {
-        switch (p.head_dim) {
-            case 64: err = launch_dma<64>(p, stream); break;
-            case 80: err = launch_dma<80>(p, stream); break;
-            case 128: err = launch_dma<128>(p, stream); break;
-            default: return hipErrorInvalidValue;
-        }
+        VCPP_PF_D(VCPP_KV_F16)
     } else {
         VCPP_PF_D(VCPP_KV_I8)
     }
