@@ -164,6 +164,24 @@ void paged_attention_cuda(const float* q, const uint16_t* kv_cache, const int32_
                           int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                           int32_t batch_size);
 
+/*
+ * cuda/attention.h:32-45 (flash_attention_cuda), contiguous K/V.  As in the
+ * reference (cuda/attention.cu:58-124), only query row 0 of each (b, h) is
+ * used and one output row per (b, h) is written:
+ *   q             [batch_size][num_heads][q_len][head_dim] fp32
+ *   k, v          [batch_size][num_heads][kv_len][head_dim] fp32
+ *   out           [batch_size][num_heads][head_dim] fp32
+ *   attn_weights  [batch_size * num_heads][kv_len] fp32, receives the softmax
+ *                 probabilities (logits * 1/sqrt(head_dim), sum + 1e-9)
+ *   attn_mask     [kv_len] fp32 or NULL; attn_mask[s] < 0 sets logit s to -1e9
+ * All pointers are device memory (the reference dereferences them on the
+ * host).  kv_len, q_len and head_dim must be > 0 (else VCPP_E_INVALID is
+ * recorded and nothing runs).  Null stream, asynchronous.
+ */
+void flash_attention_cuda(const float* q, const float* k, const float* v, float* out,
+                          float* attn_weights, int32_t batch_size, int32_t num_heads,
+                          int32_t head_dim, int32_t q_len, int32_t kv_len, const float* attn_mask);
+
 /* ---- instrumentation (no reference counterpart) --------------------------- */
 
 /* Kernel ids for vcpp_profile_read. */

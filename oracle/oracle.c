@@ -389,3 +389,41 @@ void orc_permutation(uint64_t seed, int32_t* out, int32_t n) {
         int32_t t = out[i]; out[i] = out[j]; out[j] = t;
     }
 }
+
+/* cuda/attention.cu:58-124 (host loops of flash_attention_cuda). */
+void orc_flash_attention(const float* q, const float* k, const float* v, float* out, float* w,
+                         int32_t batch, int32_t heads, int32_t head_dim, int32_t q_len,
+                         int32_t kv_len, const float* mask) {
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    for (int32_t b = 0; b < batch; ++b) {
+        for (int32_t h = 0; h < heads; ++h) {
+            const int64_t bh = (int64_t)b * heads + h;
+            const float* qr = q + bh * head_dim * q_len; /* row 0 (:90) */
+            const float* kb = k + bh * head_dim * kv_len;
+            const float* vb = v + bh * head_dim * kv_len;
+            float* lg = w + bh * kv_len;
+            for (int32_t s = 0; s < kv_len; ++s) {
+                float dot = 0.0f;
+                for (int32_t d = 0; d < head_dim; ++d) dot += qr[d] * kb[(int64_t)s * head_dim + d];
+                lg[s] = dot * scale;
+            }
+            if (mask)
+                for (int32_t s = 0; s < kv_len; ++s)
+                    if (mask[s] < 0) lg[s] = -1e9f;
+            float mx = lg[0];
+            for (int32_t s = 1; s < kv_len; ++s) mx = fmaxf(mx, lg[s]);
+            float sum = 0.0f;
+            for (int32_t s = 0; s < kv_len; ++s) {
+                lg[s] = expf(lg[s] - mx);
+                sum += lg[s];
+            }
+            for (int32_t s = 0; s < kv_len; ++s) lg[s] /= (sum + 1e-9f);
+            float* o = out + bh * head_dim;
+            for (int32_t d = 0; d < head_dim; ++d) {
+                float acc = 0.0f;
+                for (int32_t s = 0; s < kv_len; ++s) acc += lg[s] * vb[(int64_t)s * head_dim + d];
+                o[d] = acc;
+            }
+        }
+    }
+}

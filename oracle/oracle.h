@@ -78,6 +78,15 @@ void orc_prefill_batch(const orc_pool* pool, const float* q, const int32_t* tabl
 
 /* Dense fp64 softmax attention (brute force) over `n` keys for one head:
  * k, v: [n][d] fp64; returns out[d]. */
+/* Dense attention of the reference's flash_attention_cuda host loops
+ * (cuda/attention.cu:58-124): for each (b, h) only query row 0 of q
+ * [B][H][q_len][D] is used; k, v [B][H][kv_len][D]; logits * 1/sqrt(D),
+ * attn_mask[s] < 0 -> -1e9; softmax with max from logits[0], sum + 1e-9;
+ * w [B*H][kv_len] receives the probabilities, out [B][H][D]. */
+void orc_flash_attention(const float* q, const float* k, const float* v, float* out, float* w,
+                         int32_t batch, int32_t heads, int32_t head_dim, int32_t q_len,
+                         int32_t kv_len, const float* mask);
+
 void orc_dense_f64(const double* q, const double* k, const double* v, int32_t n,
                    int32_t d, double scale, double* out);
 

@@ -62,6 +62,7 @@ def orc():
         L.orc_prefill_batch.argtypes = [ctypes.POINTER(OrcPool), vp, vp, i64, vp, vp, i32, i32,
                                         vp, i32]
         L.orc_dense_f64.argtypes = [vp, vp, vp, i32, i32, ctypes.c_double, vp]
+        L.orc_flash_attention.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]
         L.orc_partial.argtypes = [ctypes.POINTER(OrcPool), vp, i32, vp, i32, i32, i32, vp, vp, vp]
         L.orc_lse_merge.argtypes = [vp, vp, vp, i32, i32, vp]
         L.orc_fill_normal.argtypes = [ctypes.c_uint64, vp, i64, ctypes.c_double, ctypes.c_double]
@@ -272,3 +273,17 @@ class RefPool:
             ref().ref_pool_destroy(self.h)
         except Exception:
             pass
+
+
+def flash(q, k, v, mask=None):
+    """orc_flash_attention on q [B][H][q_len][D], k/v [B][H][kv_len][D] (fp32);
+    returns (out [B][H][D], weights [B*H][kv_len])."""
+    q, k, v = (np.ascontiguousarray(a, np.float32) for a in (q, k, v))
+    B, H, ql, D = q.shape
+    kv = k.shape[2]
+    out = np.zeros((B, H, D), np.float32)
+    w = np.zeros((B * H, kv), np.float32)
+    m = None if mask is None else np.ascontiguousarray(mask, np.float32)
+    orc().orc_flash_attention(_p(q), _p(k), _p(v), _p(out), _p(w), B, H, D, ql, kv,
+                              None if m is None else _p(m))
+    return out, w

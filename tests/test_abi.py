@@ -88,3 +88,14 @@ def test_v1_rejects_block_size():
     ctx = (ctypes.c_int32 * 1)(16)
     L.paged_attention_cuda(4096, 4096, 4096, ctypes.addressof(ctx), 4096, 64, 8, 80, 8, 1)
     assert "block_size" in pyvcpp.last_error()
+
+
+def test_flash_rejects_empty_kv():
+    """kv_len 0 would read an unset logit in the reference; here it records
+    VCPP_E_INVALID before any HIP call."""
+    L = pyvcpp.lib()
+    dummy = ctypes.c_void_p(16)
+    L.flash_attention_cuda(dummy, dummy, dummy, dummy, dummy, 1, 1, 80, 1, 0, None)
+    assert "kv_len 0" in pyvcpp.last_error()
+    L.flash_attention_cuda(None, dummy, dummy, dummy, dummy, 1, 1, 80, 1, 4, None)
+    assert "NULL" in pyvcpp.last_error()

@@ -282,3 +282,39 @@ def test_generator_statistics():
     assert sorted(p) == list(range(1000))
     u = O.uniform_int(23, 10000, 128, 4096)
     assert u.min() >= 128 and u.max() <= 4096
+
+
+def test_flash_attention_brute_force():
+    """orc_flash_attention (cuda/attention.cu:58-124) against a float64 dense
+    softmax of query row 0; rows 1.. of q never matter."""
+    B, H, ql, kv, D = 2, 3, 4, 37, 80
+    q = O.normal(901, (B, H, ql, D))
+    k = O.normal(902, (B, H, kv, D))
+    v = O.normal(903, (B, H, kv, D))
+    out, w = O.flash(q, k, v)
+    for b in range(B):
+        for h in range(H):
+            s = k[b, h].astype(np.float64) @ q[b, h, 0].astype(np.float64) / np.sqrt(D)
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            np.testing.assert_allclose(w[b * H + h], p, atol=1e-6, rtol=1e-5)
+            np.testing.assert_allclose(out[b, h], p @ v[b, h].astype(np.float64), atol=2e-6, rtol=1e-5)
+    q2 = q.copy()
+    q2[:, :, 1:] = 123.0
+    out2, _ = O.flash(q2, k, v)
+    np.testing.assert_array_equal(out2, out)
+
+
+def test_flash_attention_mask():
+    """attn_mask[s] < 0 sets logit s to -1e9: with one position left open the
+    output is that V row and its weight is 1."""
+    B, H, kv, D = 1, 2, 9, 16
+    q = O.normal(911, (B, H, 1, D))
+    k = O.normal(912, (B, H, kv, D))
+    v = O.normal(913, (B, H, kv, D))
+    mask = -np.ones(kv, np.float32)
+    mask[5] = 0.0
+    out, w = O.flash(q, k, v, mask)
+    for h in range(H):
+        np.testing.assert_allclose(out[0, h], v[0, h, 5], atol=1e-6)
+        assert abs(w[h, 5] - 1.0) < 1e-6 and np.all(w[h, np.arange(kv) != 5] == 0.0)

@@ -17,6 +17,7 @@
 
 #include "decode.h"
 #include "prefill.h"
+#include "dense.h"
 #include "vcpp_attention.h"
 
 namespace {
@@ -372,6 +373,30 @@ void paged_attention_cuda(const float* q, const uint16_t* kv_cache, const int32_
     }
     vcpp_paged_decode(&kv, q, out, block_tables, max_blocks, nullptr, st.ctx, batch_size,
                       max_ctx, num_heads, 0, st.ws, st.ws_bytes, nullptr);
+}
+
+void flash_attention_cuda(const float* q, const float* k, const float* v, float* out,
+                          float* attn_weights, int32_t batch_size, int32_t num_heads,
+                          int32_t head_dim, int32_t q_len, int32_t kv_len, const float* attn_mask) {
+    g_last_error.clear();
+    if (batch_size <= 0 || num_heads <= 0) return;
+    if (!q || !k || !v || !out || !attn_weights) {
+        fail(VCPP_E_INVALID, "flash_attention_cuda: q/k/v/out/attn_weights is NULL");
+        return;
+    }
+    if (head_dim <= 0 || q_len <= 0 || kv_len <= 0) {
+        // kv_len 0 would make the reference read an unset logit (cuda/attention.cu:100).
+        fail(VCPP_E_INVALID, "flash_attention_cuda: head_dim %d, q_len %d, kv_len %d must be > 0",
+             head_dim, q_len, kv_len);
+        return;
+    }
+    if ((int64_t)batch_size * num_heads > INT32_MAX || head_dim > 16384) {
+        fail(VCPP_E_UNSUPPORTED, "flash_attention_cuda: shape too large");
+        return;
+    }
+    vcpp::DenseParams p{q, k, v, out, attn_weights, attn_mask, batch_size, num_heads, head_dim, q_len, kv_len};
+    const hipError_t e = vcpp::launch_dense(p, nullptr);
+    if (e != hipSuccess) hip_fail(e, "flash_attention_cuda launch");
 }
 
 }  // extern "C"

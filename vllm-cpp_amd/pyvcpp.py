@@ -30,6 +30,7 @@ EXPORTS = [
     "vcpp_decode_workspace_size",
     "vcpp_paged_prefill",
     "paged_attention_cuda",
+    "flash_attention_cuda",
     "vcpp_profile_enable",
     "vcpp_profile_read",
 ]
@@ -84,6 +85,8 @@ def lib():
     L.vcpp_paged_prefill.restype = ctypes.c_int
     L.paged_attention_cuda.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32]
     L.paged_attention_cuda.restype = None
+    L.flash_attention_cuda.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]
+    L.flash_attention_cuda.restype = None
     L.vcpp_profile_enable.argtypes = [ctypes.c_int]
     L.vcpp_profile_enable.restype = ctypes.c_int
     L.vcpp_profile_read.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
@@ -129,9 +132,9 @@ def decode_workspace_size(pages, num_seqs, num_heads, max_context_len, partition
 
 def paged_decode(pages, q, out, block_tables, context_lens, max_context_len, num_heads,
                  table_lens=None, partition_size=0, workspace=None, stream=None):
-    """vcpp_paged_decode on device tensors.  `workspace` is a zero-initialised
-    uint8 device tensor of at least decode_workspace_size(...) bytes, reused
-    across calls (allocated here when None)."""
+    """vcpp_paged_decode on device tensors.  `workspace` is a uint8 device
+    tensor of at least decode_workspace_size(...) bytes, reusable across calls
+    on one stream (allocated here when None)."""
     num_seqs = q.shape[0]
     max_blocks = block_tables.shape[1] if block_tables is not None and block_tables.dim() == 2 else 0
     need = decode_workspace_size(pages, num_seqs, num_heads, max_context_len, partition_size)
