@@ -144,6 +144,27 @@ int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
                        const int32_t* q_start, const int32_t* prefix_lens, int32_t num_chunks,
                        int32_t max_chunk_len, int32_t num_heads, void* stream);
 
+/* ---- v2: writing K/V into the pages ------------------------------------ */
+
+/*
+ * Writes num_tokens new K/V rows into the pages described by kv (which must be
+ * writable): token t goes to physical slot slots[t] = block_id * block_size +
+ * position (slots[t] < 0, or a block id >= num_blocks, skips the token).
+ *   k, v   [num_tokens][num_kv_heads][head_dim] fp32 on the device
+ *   slots  [num_tokens] int64 on the device
+ * Encoding by kv->dtype: F32 copies; F16 uses the reference encoder
+ * (src/kv_cache_manager.cpp:157-179: mantissa truncated, values below the
+ * normal range flushed to +/-0, overflow to +/-inf) unless fp16_round_nearest
+ * is non-zero (IEEE round-to-nearest-even); I8 quantises each (token, kv head)
+ * row symmetrically: scale = fp16_rne(max|x| / 127) into the scale page,
+ * values rne(x / scale) clamped to +/-127 (0 when the scale is 0).
+ * The device side of KVCacheManager::write_kv / write_kv_token /
+ * write_kv_prefill (src/kv_cache_manager.cpp:297-314,
+ * src/paged_attention.cpp:127-168), batched over tokens.
+ */
+int vcpp_write_kv(const vcpp_kv_pages* kv, const float* k, const float* v, const int64_t* slots,
+                  int32_t num_tokens, int32_t fp16_round_nearest, void* stream);
+
 /* ---- v1: reference launcher signatures (cuda/attention.h) -------------- */
 
 /*

@@ -1,0 +1,126 @@
+"""GPU parity of vcpp_write_kv (the device side of KVCacheManager::write_kv,
+src/kv_cache_manager.cpp:297-314) against the oracle's encoders: bit-exact
+pages for fp32, fp16 (reference truncation, and round-to-nearest on request)
+and int8 + fp16 scales; skipped slots leave pages untouched."""
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+import pyvcpp
+from gpu_util import DevPool, dev
+
+pytestmark = pytest.mark.gpu
+
+NB, BS, HKV, D = 12, 16, 4, 80
+
+
+def special_rows(seed, n):
+    x = O.normal(seed, (n, HKV, D), 0.0, 3.0)
+    flat = x.reshape(-1)
+    sp = np.array([0.0, -0.0, 1 + 3 * 2.0 ** -12, -(1 + 3 * 2.0 ** -12), 6.0e-5, 5.9e-8, -3.0e-8,
+                   65504.0, 65520.0, 7.0e4, -1.0e6, 2.0 ** -14, 2.0 ** -15, 1e-3, 0.33333334],
+                  np.float32)
+    flat[:sp.size] = sp
+    x[1] = 0.0          # an all-zero (token, head) row: int8 scale 0
+    x[2, 0] *= 1e-6     # tiny row
+    return x
+
+
+def empty_pool(kind):
+    shape = (NB, BS, HKV, D)
+    if kind == O.ORC_F32:
+        return O.Pool(kind, np.full(shape, 7.0, np.float32), np.full(shape, 7.0, np.float32))
+    if kind == O.ORC_F16:
+        return O.Pool(kind, np.full(shape, 0x1234, np.uint16), np.full(shape, 0x4321, np.uint16))
+    sc = np.full((NB, HKV, BS), 0x3C00, np.uint16)
+    return O.Pool(kind, np.full(shape, 5, np.int8), np.full(shape, -5, np.int8), sc, sc.copy())
+
+
+def readback(dp, kind):
+    k = dp.k.cpu().numpy()
+    v = dp.v.cpu().numpy()
+    if kind == O.ORC_F16:
+        k, v = k.view(np.uint16), v.view(np.uint16)
+    if kind == O.ORC_I8:
+        return k, v, dp.ks.cpu().numpy().view(np.uint16), dp.vs.cpu().numpy().view(np.uint16)
+    return k, v, None, None
+
+
+@pytest.mark.parametrize("kind,rne", [(O.ORC_F32, 0), (O.ORC_F16, 0), (O.ORC_F16, 1), (O.ORC_I8, 0)])
+def test_write_kv_bit_exact(cuda, kind, rne):
+    n = 40
+    k = special_rows(71, n)
+    v = special_rows(72, n)
+    slots = O.permutation(73, NB * BS)[:n].astype(np.int64)
+    slots[5] = -1                 # skipped
+    slots[6] = NB * BS + 3        # block past the pool: skipped
+    pool = empty_pool(kind)
+    dp = DevPool(pool)
+    pyvcpp.write_kv(dp.pages, dev(k), dev(v), dev(slots), fp16_round_nearest=bool(rne))
+    torch.cuda.synchronize()
+    gk, gv, gks, gvs = readback(dp, kind)
+    wk, wv = pool.k.copy(), pool.v.copy()
+    wks = None if pool.k_scale is None else pool.k_scale.copy()
+    wvs = None if pool.v_scale is None else pool.v_scale.copy()
+    for t in range(n):
+        s = int(slots[t])
+        if s < 0 or s >= NB * BS:
+            continue
+        b, p = divmod(s, BS)
+        for src, dst, sdst in ((k[t], wk, wks), (v[t], wv, wvs)):
+            if kind == O.ORC_F32:
+                dst[b, p] = src
+            elif kind == O.ORC_F16:
+                dst[b, p] = src.astype(np.float16).view(np.uint16) if rne else O.f16_trunc(src)
+            else:
+                q, sc = O.quant_i8(src)
+                dst[b, p] = q
+                sdst[b, :, p] = sc
+    np.testing.assert_array_equal(gk, wk)
+    np.testing.assert_array_equal(gv, wv)
+    if kind == O.ORC_I8:
+        np.testing.assert_array_equal(gks, wks)
+        np.testing.assert_array_equal(gvs, wvs)
+
+
+@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8])
+def test_write_then_prefill(cuda, kind):
+    """Pages written on the device from fp32 K/V, then a causal prefill over
+    them, equal the oracle on pages the oracle encoded itself."""
+    from gpu_util import assert_close, gpu_prefill
+    H, Hkv, Dd = 16, 2, 80
+    lens = [150, 37]
+    nb = 24
+    k = O.normal(81, (sum(lens), Hkv, Dd))
+    v = O.normal(82, (sum(lens), Hkv, Dd))
+    tables = O.permutation(83, nb)[:20].reshape(2, 10).astype(np.int32)
+    slots = np.concatenate([tables[i, np.arange(n) // 16] * 16 + np.arange(n) % 16
+                            for i, n in enumerate(lens)]).astype(np.int64)
+    shape = (nb, 16, Hkv, Dd)
+    if kind == O.ORC_F16:
+        host = O.Pool(kind, np.zeros(shape, np.uint16), np.zeros(shape, np.uint16))
+    else:
+        host = O.Pool(kind, np.zeros(shape, np.int8), np.zeros(shape, np.int8),
+                      np.zeros((nb, Hkv, 16), np.uint16), np.zeros((nb, Hkv, 16), np.uint16))
+    dp = DevPool(host)
+    pyvcpp.write_kv(dp.pages, dev(k), dev(v), dev(slots))
+    torch.cuda.synchronize()
+    gk, gv, gks, gvs = readback(dp, kind)
+    # oracle pages from the same rows
+    for t, s in enumerate(slots):
+        b, p = divmod(int(s), 16)
+        if kind == O.ORC_F16:
+            host.k[b, p], host.v[b, p] = O.f16_trunc(k[t]), O.f16_trunc(v[t])
+        else:
+            (host.k[b, p], host.k_scale[b, :, p]), (host.v[b, p], host.v_scale[b, :, p]) = \
+                O.quant_i8(k[t]), O.quant_i8(v[t])
+    np.testing.assert_array_equal(gk, host.k)
+    np.testing.assert_array_equal(gv, host.v)
+    q_start = np.array([0, 50, 60], np.int32)
+    prefix = np.array([lens[0] - 50, lens[1] - 10], np.int32)
+    q32 = O.normal(84, (60, H, Dd))
+    q16 = q32.astype(np.float16)
+    want = O.prefill(host, q16.astype(np.float32), tables, q_start, prefix, H)
+    got = gpu_prefill(dp, q16.view(np.uint16), tables, q_start, prefix, H)
+    assert_close(got, want, 2e-3, 1e-2, what="write then prefill kind=%d" % kind)

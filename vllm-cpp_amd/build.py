@@ -11,8 +11,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libvcpp_attn.so")
-SOURCES = ["csrc/decode.hip", "csrc/prefill.hip", "csrc/dense.hip", "csrc/api.cpp", "csrc/profile.cpp"]
-HEADERS = ["csrc/decode.h", "csrc/prefill.h", "csrc/dense.h", "csrc/device_common.h", "csrc/profile.h"]
+SOURCES = ["csrc/decode.hip", "csrc/prefill.hip", "csrc/dense.hip", "csrc/kv_write.hip", "csrc/api.cpp", "csrc/profile.cpp"]
+HEADERS = ["csrc/decode.h", "csrc/prefill.h", "csrc/dense.h", "csrc/kv_write.h", "csrc/device_common.h", "csrc/profile.h"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

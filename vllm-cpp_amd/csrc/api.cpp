@@ -18,6 +18,7 @@
 #include "decode.h"
 #include "prefill.h"
 #include "dense.h"
+#include "kv_write.h"
 #include "vcpp_attention.h"
 
 namespace {
@@ -308,6 +309,38 @@ int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
     p.bs_magic = ((1ull << 40) + kv->block_size - 1) / kv->block_size;
     hipError_t e = vcpp::launch_prefill(p, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "prefill launch");
+    return VCPP_OK;
+}
+
+int vcpp_write_kv(const vcpp_kv_pages* kv, const float* k, const float* v, const int64_t* slots,
+                  int32_t num_tokens, int32_t fp16_round_nearest, void* stream) {
+    g_last_error.clear();
+    int rc = check_pages(kv);
+    if (rc != VCPP_OK) return rc;
+    if (num_tokens < 0) return fail(VCPP_E_INVALID, "num_tokens must be >= 0");
+    if (num_tokens == 0) return VCPP_OK;
+    if (!k || !v || !slots) return fail(VCPP_E_INVALID, "k/v/slots is NULL");
+    if ((int64_t)num_tokens * kv->num_kv_heads > (int64_t)INT32_MAX * 4)
+        return fail(VCPP_E_UNSUPPORTED, "too many tokens (%d)", num_tokens);
+    vcpp::KvWriteParams p{};
+    p.dtype = kv->dtype;
+    p.block_size = kv->block_size;
+    p.num_kv_heads = kv->num_kv_heads;
+    p.head_dim = kv->head_dim;
+    p.num_blocks = kv->num_blocks;
+    p.block_stride = kv->block_stride;
+    p.scale_block_stride = kv->scale_block_stride;
+    p.k = const_cast<void*>(kv->k);  // the pages are written: they must be writable
+    p.v = const_cast<void*>(kv->v);
+    p.k_scale = const_cast<uint16_t*>(kv->k_scale);
+    p.v_scale = const_cast<uint16_t*>(kv->v_scale);
+    p.k_src = k;
+    p.v_src = v;
+    p.slots = slots;
+    p.num_tokens = num_tokens;
+    p.fp16_rne = fp16_round_nearest ? 1 : 0;
+    const hipError_t e = vcpp::launch_kv_write(p, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "write_kv launch");
     return VCPP_OK;
 }
 

@@ -29,6 +29,7 @@ EXPORTS = [
     "vcpp_paged_decode",
     "vcpp_decode_workspace_size",
     "vcpp_paged_prefill",
+    "vcpp_write_kv",
     "paged_attention_cuda",
     "flash_attention_cuda",
     "vcpp_profile_enable",
@@ -83,6 +84,8 @@ def lib():
     L.vcpp_paged_prefill.argtypes = [ctypes.POINTER(KVPages), vp, vp, vp, i32, vp, vp, i32, i32,
                                      i32, vp]
     L.vcpp_paged_prefill.restype = ctypes.c_int
+    L.vcpp_write_kv.argtypes = [ctypes.POINTER(KVPages), vp, vp, vp, i32, i32, vp]
+    L.vcpp_write_kv.restype = ctypes.c_int
     L.paged_attention_cuda.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32]
     L.paged_attention_cuda.restype = None
     L.flash_attention_cuda.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]
@@ -170,3 +173,10 @@ def paged_prefill(pages, q, out, block_tables, q_start, prefix_lens, max_chunk_l
                                   prefix_lens.shape[0], max_chunk_len, num_heads, _stream(stream))
     _check(rc)
     return out
+
+
+def write_kv(pages, k, v, slots, fp16_round_nearest=False, stream=None):
+    """vcpp_write_kv: k, v fp32 [n][Hkv][D] and slots int64 [n] device tensors."""
+    rc = lib().vcpp_write_kv(ctypes.byref(pages), _ptr(k), _ptr(v), _ptr(slots), k.shape[0],
+                             1 if fp16_round_nearest else 0, _stream(stream))
+    _check(rc)
