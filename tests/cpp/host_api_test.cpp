@@ -1,0 +1,289 @@
+// host_api_test.cpp -- drives the C++ BlockPool / KVCacheManager /
+// paged_attention mirror (include/vllm_cpp) the way the reference engine
+// does (src/paged_engine.cpp:329-384,460-508) and checks every result
+// against the CPU oracle (oracle/oracle.h) on the same data.  Test
+// infrastructure: links liboracle.so as the checker.
+//
+// Prints one line per check and "ALL PASSED" at the end; exit status 1 on
+// the first failure.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <random>
+#include <vector>
+
+#include "oracle.h"
+#include "vllm_cpp/paged_attention.h"
+
+namespace {
+
+int g_checks = 0;
+
+#define CHECK(cond, ...)                                                   \
+    do {                                                                   \
+        ++g_checks;                                                        \
+        if (!(cond)) {                                                     \
+            std::printf("FAIL %s:%d: ", __FILE__, __LINE__);               \
+            std::printf(__VA_ARGS__);                                      \
+            std::printf("\n");                                             \
+            std::exit(1);                                                  \
+        }                                                                  \
+    } while (0)
+
+std::vector<float> normal(uint64_t seed, size_t n, double std = 1.0) {
+    std::vector<float> x(n);
+    orc_fill_normal(seed, x.data(), (int64_t)n, 0.0, std);
+    return x;
+}
+
+void close(const float* got, const float* want, size_t n, double atol, double rtol, const char* what) {
+    double worst = 0;
+    for (size_t i = 0; i < n; ++i) {
+        const double err = std::fabs((double)got[i] - want[i]);
+        CHECK(std::isfinite(got[i]), "%s: non-finite at %zu", what, i);
+        CHECK(err <= atol + rtol * std::fabs((double)want[i]), "%s: index %zu got %.7g want %.7g", what,
+              i, got[i], want[i]);
+        worst = std::max(worst, err);
+    }
+    std::printf("ok   %-58s max abs err %.3g\n", what, worst);
+}
+
+// Host image of one layer of a pool in the reference slab layout, encoded by
+// the oracle, for orc_paged_attention.
+struct HostLayer {
+    KVDtype dtype;
+    int32_t nb, num_layers, hkv, d;
+    std::vector<uint8_t> k, v;       // [nb][num_layers][16][kv_dim] elements
+    std::vector<uint16_t> ks, vs;    // [nb][num_layers][hkv][16]
+    HostLayer(KVDtype t, int32_t nb_, int32_t nl, int32_t hkv_, int32_t d_)
+        : dtype(t), nb(nb_), num_layers(nl), hkv(hkv_), d(d_) {
+        const size_t n = (size_t)nb * nl * 16 * hkv * d * kv_elem_size(t);
+        k.assign(n, 0);
+        v.assign(n, 0);
+        ks.assign((size_t)nb * nl * hkv * 16, 0);
+        vs.assign((size_t)nb * nl * hkv * 16, 0);
+    }
+    int64_t row_off(int32_t block, int32_t layer, int32_t pos) const {
+        return (((int64_t)block * num_layers + layer) * 16 + pos) * hkv * d;  // elements
+    }
+    void write(int32_t block, int32_t layer, int32_t pos, const float* kr, const float* vr) {
+        const int64_t off = row_off(block, layer, pos);
+        for (int which = 0; which < 2; ++which) {
+            const float* src = which ? vr : kr;
+            std::vector<uint8_t>& dst = which ? v : k;
+            if (dtype == KVDtype::FP32) {
+                std::memcpy(dst.data() + off * 4, src, sizeof(float) * hkv * d);
+            } else if (dtype == KVDtype::FP16) {
+                orc_f16_encode_trunc_n(src, reinterpret_cast<uint16_t*>(dst.data()) + off, (int64_t)hkv * d);
+            } else {
+                std::vector<uint16_t>& sc = which ? vs : ks;
+                for (int32_t h = 0; h < hkv; ++h) {
+                    uint16_t s;
+                    orc_quant_i8(src + h * d, d, reinterpret_cast<int8_t*>(dst.data()) + off + h * d, &s);
+                    sc[(((int64_t)block * num_layers + layer) * hkv + h) * 16 + pos] = s;
+                }
+            }
+        }
+    }
+    orc_pool pool(int32_t layer) const {
+        orc_pool p{};
+        p.kind = dtype == KVDtype::FP32 ? ORC_F32 : dtype == KVDtype::FP16 ? ORC_F16 : ORC_I8;
+        const int64_t esz = kv_elem_size(dtype);
+        p.k = k.data() + (int64_t)layer * 16 * hkv * d * esz;
+        p.v = v.data() + (int64_t)layer * 16 * hkv * d * esz;
+        p.k_scale = ks.data() + (int64_t)layer * hkv * 16;
+        p.v_scale = vs.data() + (int64_t)layer * hkv * 16;
+        p.num_blocks = nb;
+        p.block_stride = (int64_t)num_layers * 16 * hkv * d;
+        p.scale_block_stride = (int64_t)num_layers * hkv * 16;
+        p.block_size = 16;
+        p.num_kv_heads = hkv;
+        p.head_dim = d;
+        return p;
+    }
+};
+
+void test_bookkeeping() {
+    BlockPool pool(6, 2, 32, KVDtype::FP32);
+    CHECK(pool.alloc() == 0 && pool.alloc() == 1 && pool.alloc() == 2, "alloc order");
+    CHECK(pool.free_count() == 3 && pool.used_count() == 3, "counts");
+    pool.ref(1);
+    pool.free(1);  // ref 2 -> 1: still used
+    CHECK(!pool.get_block(1).free && pool.get_block(1).ref_count == 1, "free with ref");
+    pool.deref(1);
+    CHECK(pool.get_block(1).free, "deref to zero frees");
+    CHECK(pool.alloc() == 1, "lowest free block first");
+    pool.free(-3);
+    pool.free(99);  // out of range: ignored
+    CHECK(pool.used_count() == 3, "out-of-range free ignored");
+    CHECK(pool.get_k_raw(6, 0) == nullptr && pool.get_k_raw(0, 2) == nullptr, "raw bounds");
+    CHECK(pool.get_k_raw(1, 1) == pool.get_k_raw(1, 0) + 16 * 32 * 4, "layer slab offset");
+    CHECK(pool.get_k_raw(2, 0) == pool.get_k_raw(1, 0) + 2 * 16 * 32 * 4, "block offset");
+    pool.reset();
+    CHECK(pool.free_count() == 6, "reset frees all");
+    std::printf("ok   %-58s\n", "BlockPool book-keeping (alloc/free/ref/deref/reset)");
+}
+
+void test_write_read(KVDtype dt) {
+    const int32_t L = 3, H = 4, D = 80, kv = H * D;
+    KVCacheManager m(L, kv, 5, dt, D);
+    HostLayer host(dt, 5, L, H, D);
+    std::vector<int32_t> blocks;
+    CHECK(m.alloc_blocks(3, blocks), "alloc_blocks");
+    auto k = normal(11, kv * 4, 2.0), v = normal(12, kv * 4, 2.0);
+    const int32_t pos[4] = {0, 5, 15, 7};
+    for (int i = 0; i < 4; ++i) {
+        m.write_kv(blocks[i % 3], i % L, pos[i], k.data() + i * kv, v.data() + i * kv, kv);
+        host.write(blocks[i % 3], i % L, pos[i], k.data() + i * kv, v.data() + i * kv);
+    }
+    m.write_kv(blocks[0], 0, 16, k.data(), v.data(), kv);  // slot out of range: ignored
+    m.write_kv(77, 0, 0, k.data(), v.data(), kv);          // block out of range: ignored
+    // Raw device bytes equal the oracle's encoding.
+    const BlockPool& p = m.block_pool();
+    for (int32_t b = 0; b < 5; ++b)
+        for (int32_t l = 0; l < L; ++l) {
+            const size_t bytes = (size_t)16 * kv * kv_elem_size(dt);
+            std::vector<uint8_t> got(bytes);
+            CHECK(hipMemcpy(got.data(), p.get_k_raw(b, l), bytes, hipMemcpyDeviceToHost) == hipSuccess, "copy");
+            CHECK(std::memcmp(got.data(), host.k.data() + host.row_off(b, l, 0) * kv_elem_size(dt), bytes) == 0,
+                  "K bytes of block %d layer %d", b, l);
+        }
+    // read_kv returns the decoded values.
+    std::vector<float> rk(kv), rv(kv);
+    for (int i = 0; i < 4; ++i) {
+        m.read_kv(blocks[i % 3], i % L, pos[i], rk.data(), rv.data(), kv);
+        orc_pool op = host.pool(i % L);
+        std::vector<float> want(kv);
+        for (int32_t j = 0; j < kv; ++j) {
+            if (dt == KVDtype::FP32) want[j] = k[i * kv + j];
+            else if (dt == KVDtype::FP16) want[j] = orc_f16_decode(orc_f16_encode_trunc(k[i * kv + j]));
+            else {
+                const int32_t h = j / D;
+                const int8_t q = reinterpret_cast<const int8_t*>(op.k)[blocks[i % 3] * op.block_stride + pos[i] * kv + j];
+                want[j] = (float)q * orc_f16_decode(op.k_scale[blocks[i % 3] * op.scale_block_stride + h * 16 + pos[i]]);
+            }
+        }
+        CHECK(std::memcmp(rk.data(), want.data(), sizeof(float) * kv) == 0, "read_kv row %d", i);
+    }
+    // free zeroes the block; copy_blocks copies all layers.
+    m.copy_blocks({blocks[1]}, {blocks[2]});
+    std::vector<float> a(kv), b2(kv), c(kv);
+    m.read_kv(blocks[2], 1, pos[1], a.data(), b2.data(), kv);
+    m.read_kv(blocks[1], 1, pos[1], c.data(), b2.data(), kv);
+    CHECK(std::memcmp(a.data(), c.data(), sizeof(float) * kv) == 0, "copy_blocks");
+    m.free_blocks({blocks[0]});
+    m.read_kv(blocks[0], 0, pos[0], a.data(), b2.data(), kv);
+    bool zero = true;
+    for (float x : a) zero &= (x == 0.0f);
+    CHECK(zero, "freed block zeroed");
+    static const char* names[] = {"FP32", "FP16", "FP8", "INT8"};
+    std::printf("ok   write_kv / read_kv / copy_blocks / free on %-12s (bit-exact)\n", names[(int)dt]);
+}
+
+void test_attention(KVDtype dt) {
+    const int32_t L = 2, layer = 1, H = 64, HKV = 8, D = 80, kv = HKV * D, NB = 160;
+    KVCacheManager m(L, kv, NB, dt, D);
+    HostLayer host(dt, NB, L, HKV, D);
+    // Reserve a few blocks so tables are not the identity.
+    std::vector<int32_t> junk;
+    CHECK(m.alloc_blocks(7, junk), "alloc");
+    const int32_t lens[4] = {1, 300, 17, 777};
+    std::vector<std::vector<int32_t>> tables(4);
+    std::vector<std::vector<float>> ks, vs;
+    for (int r = 0; r < 4; ++r) {
+        CHECK(m.alloc_blocks((lens[r] + 15) / 16 + 1, tables[r]), "alloc request %d", r);
+        ks.push_back(normal(100 + r, (size_t)lens[r] * kv));
+        vs.push_back(normal(200 + r, (size_t)lens[r] * kv));
+        // prefill all but the last token, then append it as a decode step
+        write_kv_prefill(m, tables[r], lens[r] - 1, layer, ks[r].data(), vs[r].data());
+        write_kv_token(m, tables[r], lens[r], layer, ks[r].data() + (size_t)(lens[r] - 1) * kv,
+                       vs[r].data() + (size_t)(lens[r] - 1) * kv);
+        for (int32_t p = 0; p < lens[r]; ++p)
+            host.write(tables[r][p / 16], layer, p % 16, ks[r].data() + (size_t)p * kv,
+                       vs[r].data() + (size_t)p * kv);
+        tables[r].pop_back();  // one spare block removed: table covers exactly the context
+    }
+    tables[2][0] = NB + 5;     // a bad block id: skipped by both sides
+    const double tol = dt == KVDtype::FP32 ? 1e-4 : 2e-3, rtol = dt == KVDtype::FP32 ? 1e-4 : 1e-2;
+    orc_pool op = host.pool(layer);
+    std::vector<float> q = normal(300, (size_t)4 * H * D), want((size_t)4 * H * D);
+    for (int r = 0; r < 4; ++r)
+        orc_paged_attention(&op, q.data() + (size_t)r * H * D, tables[r].data(), (int32_t)tables[r].size(),
+                            lens[r], H, want.data() + (size_t)r * H * D);
+    // 1. one request at a time, host buffers (the reference engine's call)
+    std::vector<float> out((size_t)4 * H * D, NAN);
+    for (int r = 0; r < 4; ++r)
+        paged_attention(q.data() + (size_t)r * H * D, tables[r], lens[r], m.block_pool(), H, HKV, D, layer,
+                        out.data() + (size_t)r * H * D);
+    close(out.data(), want.data(), out.size(), tol, rtol, "paged_attention, host buffers");
+    // 2. one launch for the batch, device buffers
+    float *qd, *od;
+    CHECK(hipMalloc(&qd, q.size() * 4) == hipSuccess && hipMalloc(&od, q.size() * 4) == hipSuccess, "malloc");
+    CHECK(hipMemcpy(qd, q.data(), q.size() * 4, hipMemcpyHostToDevice) == hipSuccess, "copy");
+    std::vector<const float*> qp;
+    std::vector<float*> opp;
+    std::vector<const std::vector<int32_t>*> tp;
+    std::vector<int32_t> sl;
+    for (int r = 0; r < 4; ++r) {
+        qp.push_back(qd + (size_t)r * H * D);
+        opp.push_back(od + (size_t)r * H * D);
+        tp.push_back(&tables[r]);
+        sl.push_back(lens[r]);
+    }
+    paged_attention_batch(qp, tp, sl, m.block_pool(), H, HKV, D, layer, opp);
+    CHECK(hipDeviceSynchronize() == hipSuccess, "sync");
+    std::vector<float> out2(q.size());
+    CHECK(hipMemcpy(out2.data(), od, q.size() * 4, hipMemcpyDeviceToHost) == hipSuccess, "copy");
+    close(out2.data(), want.data(), out2.size(), tol, rtol, "paged_attention_batch, device buffers");
+    // 3. a null table is skipped: its output stays untouched
+    std::vector<float> keep(H * D, 42.0f);
+    std::vector<const float*> q3{q.data(), q.data() + H * D};
+    std::vector<float*> o3{out.data(), keep.data()};
+    std::vector<const std::vector<int32_t>*> t3{&tables[0], nullptr};
+    paged_attention_batch(q3, t3, {lens[0], lens[1]}, m.block_pool(), H, HKV, D, layer, o3);
+    CHECK(keep[0] == 42.0f && keep[H * D - 1] == 42.0f, "null table skipped");
+    // 4. a table shorter than seq_len: positions past it are skipped
+    std::vector<int32_t> short_t(tables[3].begin(), tables[3].begin() + 10);
+    std::vector<float> w4(H * D), g4(H * D);
+    orc_paged_attention(&op, q.data(), short_t.data(), 10, lens[3], H, w4.data());
+    paged_attention(q.data(), short_t, lens[3], m.block_pool(), H, HKV, D, layer, g4.data());
+    close(g4.data(), w4.data(), g4.size(), tol, rtol, "paged_attention, table shorter than seq_len");
+    // 5. read_kv_prefill gathers the decoded rows
+    std::vector<float> rk((size_t)lens[1] * kv), rv((size_t)lens[1] * kv);
+    read_kv_prefill(m.block_pool(), tables[1], lens[1], layer, HKV, D, rk.data(), rv.data());
+    for (int32_t p = 0; p < lens[1]; p += 37) {
+        for (int32_t j = 0; j < kv; j += 13) {
+            float want_k;
+            const int64_t e = tables[1][p / 16] * op.block_stride + (int64_t)(p % 16) * kv + j;
+            if (dt == KVDtype::FP32) want_k = reinterpret_cast<const float*>(op.k)[e];
+            else if (dt == KVDtype::FP16) want_k = orc_f16_decode(reinterpret_cast<const uint16_t*>(op.k)[e]);
+            else want_k = (float)reinterpret_cast<const int8_t*>(op.k)[e] *
+                          orc_f16_decode(op.k_scale[tables[1][p / 16] * op.scale_block_stride + (j / D) * 16 + p % 16]);
+            CHECK(rk[(size_t)p * kv + j] == want_k, "read_kv_prefill pos %d dim %d", p, j);
+        }
+    }
+    std::printf("ok   %-58s\n", "read_kv_prefill");
+    (void)hipFree(qd);
+    (void)hipFree(od);
+}
+
+}  // namespace
+
+int main() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+        std::printf("no GPU\n");
+        return 2;
+    }
+    test_bookkeeping();
+    for (KVDtype dt : {KVDtype::FP32, KVDtype::FP16, KVDtype::INT8}) test_write_read(dt);
+    for (KVDtype dt : {KVDtype::FP32, KVDtype::FP16, KVDtype::INT8}) {
+        std::printf("---- attention on %s pages\n", dt == KVDtype::FP32 ? "FP32" : dt == KVDtype::FP16 ? "FP16" : "INT8");
+        test_attention(dt);
+    }
+    std::printf("ALL PASSED (%d checks)\n", g_checks);
+    return 0;
+}

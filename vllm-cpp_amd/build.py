@@ -11,8 +11,9 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libvcpp_attn.so")
-SOURCES = ["csrc/decode.hip", "csrc/prefill.hip", "csrc/dense.hip", "csrc/kv_write.hip", "csrc/api.cpp", "csrc/profile.cpp"]
-HEADERS = ["csrc/decode.h", "csrc/prefill.h", "csrc/dense.h", "csrc/kv_write.h", "csrc/device_common.h", "csrc/profile.h"]
+SOURCES = ["csrc/decode.hip", "csrc/prefill.hip", "csrc/dense.hip", "csrc/kv_write.hip", "csrc/api.cpp",
+           "csrc/profile.cpp", "host/kv_cache_manager.cpp", "host/paged_attention.cpp"]
+HEADERS = ["host/host_util.h", "csrc/decode.h", "csrc/prefill.h", "csrc/dense.h", "csrc/kv_write.h", "csrc/device_common.h", "csrc/profile.h"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -55,6 +56,19 @@ def build(verbose=False, out=LIB, defines=()):
         _run([HIPCC] + FLAGS + dflags + lang + ["-c", os.path.join(HERE, src), "-o", obj], verbose)
         objs.append(obj)
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", out] + objs, verbose)
+    return out
+
+
+def build_host_test(verbose=False):
+    """tests/cpp/host_api_test: the C++ BlockPool / KVCacheManager /
+    paged_attention checks, linked against this library and the CPU oracle
+    (oracle/liboracle.so, which must be built first)."""
+    src = os.path.join(ROOT, "tests", "cpp", "host_api_test.cpp")
+    out = os.path.join(ROOT, "tests", "cpp", "host_api_test")
+    _run([HIPCC, "--offload-arch=gfx950", "-O2", "-std=c++17", "-Wall",
+          "-I", os.path.join(ROOT, "include"), "-I", os.path.join(ROOT, "oracle"), src,
+          "-o", out, "-L", HERE, "-lvcpp_attn", "-L", os.path.join(ROOT, "oracle"), "-loracle",
+          "-Wl,-rpath,$ORIGIN/../../vllm-cpp_amd", "-Wl,-rpath,$ORIGIN/../../oracle"], verbose)
     return out
 
 

@@ -315,8 +315,19 @@ int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
 int vcpp_write_kv(const vcpp_kv_pages* kv, const float* k, const float* v, const int64_t* slots,
                   int32_t num_tokens, int32_t fp16_round_nearest, void* stream) {
     g_last_error.clear();
-    int rc = check_pages(kv);
-    if (rc != VCPP_OK) return rc;
+    // Writing needs less than attention: any head split and block size.
+    if (!kv) return fail(VCPP_E_INVALID, "kv pages descriptor is NULL");
+    if (kv->dtype != VCPP_KV_F32 && kv->dtype != VCPP_KV_F16 && kv->dtype != VCPP_KV_I8)
+        return fail(VCPP_E_INVALID, "unknown kv dtype %d", kv->dtype);
+    if (kv->block_size <= 0 || kv->num_kv_heads <= 0 || kv->head_dim <= 0 || kv->num_blocks < 0)
+        return fail(VCPP_E_INVALID, "bad page shape");
+    if (kv->block_stride < (int64_t)kv->block_size * kv->num_kv_heads * kv->head_dim)
+        return fail(VCPP_E_INVALID, "block_stride %lld smaller than one page", (long long)kv->block_stride);
+    if (kv->num_blocks > 0 && (!kv->k || !kv->v)) return fail(VCPP_E_INVALID, "K/V page base is NULL");
+    if (kv->dtype == VCPP_KV_I8 && kv->num_blocks > 0 &&
+        (!kv->k_scale || !kv->v_scale ||
+         kv->scale_block_stride < (int64_t)kv->num_kv_heads * kv->block_size))
+        return fail(VCPP_E_INVALID, "int8 pages need scale pages of num_kv_heads * block_size per block");
     if (num_tokens < 0) return fail(VCPP_E_INVALID, "num_tokens must be >= 0");
     if (num_tokens == 0) return VCPP_OK;
     if (!k || !v || !slots) return fail(VCPP_E_INVALID, "k/v/slots is NULL");

@@ -1,0 +1,82 @@
+// host_util.h -- helpers shared by the host-side BlockPool / KVCacheManager /
+// paged_attention implementation.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+namespace vcpp_host {
+
+inline void check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+inline void check_rc(int rc, const char* what) {
+    if (rc != 0) throw std::runtime_error(std::string(what) + ": " + vcpp_last_error());
+}
+
+// True for device (or managed) memory; plain host memory -- pageable, which
+// the runtime does not know, or pinned -- is false.
+inline bool is_device(const void* p) {
+    if (!p) return false;
+    hipPointerAttribute_t a{};
+    const hipError_t e = hipPointerGetAttributes(&a, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();  // an unknown host pointer is not an error here
+        return false;
+    }
+    return a.type == hipMemoryTypeDevice || a.type == hipMemoryTypeManaged;
+}
+
+// The reference's fp16 -> fp32 decoder (src/kv_cache_manager.cpp:120-143):
+// exact for zeros, subnormals and normals; exponent 31 gives +/-inf.
+inline float f16_decode(uint16_t h) {
+    const uint32_t s = (h >> 15) & 1u, e = (h >> 10) & 0x1Fu;
+    uint32_t f = h & 0x3FFu;
+    uint32_t bits;
+    if (e == 0) {
+        if (f == 0) {
+            bits = s << 31;
+        } else {
+            int ee = 1;
+            while ((f & 0x400u) == 0) {
+                f <<= 1;
+                --ee;
+            }
+            f &= 0x3FFu;
+            bits = (s << 31) | ((uint32_t)(127 - 15 + ee) << 23) | (f << 13);
+        }
+    } else if (e == 31) {
+        bits = (s << 31) | 0x7F800000u;
+    } else {
+        bits = (s << 31) | ((127 - 15 + e) << 23) | (f << 13);
+    }
+    float out;
+    std::memcpy(&out, &bits, 4);
+    return out;
+}
+
+// A device buffer that only grows.
+struct DevBuf {
+    void* p = nullptr;
+    size_t n = 0;
+    void* get(size_t bytes) {
+        if (bytes > n) {
+            if (p) (void)hipFree(p);
+            p = nullptr;
+            n = 0;
+            check(hipMalloc(&p, bytes), "device scratch allocation");
+            n = bytes;
+        }
+        return p;
+    }
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+};
+
+}  // namespace vcpp_host

@@ -1,0 +1,328 @@
+// kv_cache_manager.cpp -- BlockPool / KVCacheManager on device memory with the
+// interface and book-keeping of the reference src/kv_cache_manager.cpp.
+#include "vllm_cpp/kv_cache_manager.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <stdexcept>
+
+#include "host_util.h"
+
+using vcpp_host::check;
+
+namespace {
+
+// Bit-exact float view of one block layer slab (host copy of the raw bytes).
+void decode_rows(const uint8_t* raw, const uint16_t* scales, float* out, int32_t kv_dim,
+                 int32_t head_dim, KVDtype dtype) {
+    const int32_t n = BLOCK_SIZE * kv_dim;
+    switch (dtype) {
+        case KVDtype::FP32:
+            std::memcpy(out, raw, sizeof(float) * n);
+            break;
+        case KVDtype::FP16: {
+            const uint16_t* h = reinterpret_cast<const uint16_t*>(raw);
+            for (int32_t i = 0; i < n; ++i) out[i] = vcpp_host::f16_decode(h[i]);
+            break;
+        }
+        case KVDtype::INT8: {
+            const int8_t* q = reinterpret_cast<const int8_t*>(raw);
+            const int32_t hkv = kv_dim / head_dim;
+            for (int32_t t = 0; t < BLOCK_SIZE; ++t)
+                for (int32_t h = 0; h < hkv; ++h) {
+                    const float s = vcpp_host::f16_decode(scales[h * BLOCK_SIZE + t]);
+                    for (int32_t d = 0; d < head_dim; ++d) {
+                        const int32_t i = (t * hkv + h) * head_dim + d;
+                        out[i] = (float)q[i] * s;
+                    }
+                }
+            break;
+        }
+        default:
+            throw std::invalid_argument("unsupported KV dtype");
+    }
+}
+
+}  // namespace
+
+// ---- BlockPool --------------------------------------------------------------
+
+BlockPool::BlockPool(int32_t num_blocks, int32_t num_layers, int32_t kv_dim, KVDtype kv_dtype,
+                     int32_t head_dim)
+    : kv_dim_(kv_dim), num_layers_(num_layers), kv_dtype_(kv_dtype),
+      head_dim_(head_dim > 0 ? head_dim : kv_dim) {
+    if (kv_dtype == KVDtype::FP8_E4M3)
+        throw std::invalid_argument("BlockPool: FP8_E4M3 pages are not supported on the GPU");
+    if (num_blocks < 0 || num_layers <= 0 || kv_dim <= 0 || kv_dim % head_dim_ != 0)
+        throw std::invalid_argument("BlockPool: bad shape");
+    if (kv_dtype == KVDtype::INT8 && head_dim <= 0)
+        throw std::invalid_argument("BlockPool: INT8 pools need head_dim");
+    layer_bytes_ = (int64_t)BLOCK_SIZE * kv_dim * kv_elem_size(kv_dtype);
+    block_bytes_ = (int64_t)num_layers * layer_bytes_;
+    scale_layer_ = (int64_t)(kv_dim / head_dim_) * BLOCK_SIZE;
+    blocks_.resize(num_blocks);
+    for (int32_t i = 0; i < num_blocks; ++i) {
+        blocks_[i].block_id = i;
+        blocks_[i].dtype = kv_dtype;
+    }
+    const size_t bytes = (size_t)block_bytes_ * (size_t)std::max(num_blocks, 1);
+    check(hipMalloc(&k_, bytes), "BlockPool K pages");
+    check(hipMalloc(&v_, bytes), "BlockPool V pages");
+    check(hipMemset(k_, 0, bytes), "BlockPool zero K");
+    check(hipMemset(v_, 0, bytes), "BlockPool zero V");
+    if (kv_dtype == KVDtype::INT8) {
+        const size_t sb = sizeof(uint16_t) * scale_layer_ * num_layers * std::max(num_blocks, 1);
+        check(hipMalloc(&k_scale_, sb), "BlockPool K scales");
+        check(hipMalloc(&v_scale_, sb), "BlockPool V scales");
+        check(hipMemset(k_scale_, 0, sb), "BlockPool zero K scales");
+        check(hipMemset(v_scale_, 0, sb), "BlockPool zero V scales");
+    }
+    k_convert_buf_.resize((size_t)BLOCK_SIZE * kv_dim);
+    v_convert_buf_.resize((size_t)BLOCK_SIZE * kv_dim);
+}
+
+BlockPool::~BlockPool() {
+    for (void* p : {(void*)k_, (void*)v_, (void*)k_scale_, (void*)v_scale_})
+        if (p) (void)hipFree(p);
+}
+
+int32_t BlockPool::alloc() {
+    std::lock_guard<std::mutex> lock(mtx_);
+    for (int32_t i = 0; i < (int32_t)blocks_.size(); ++i) {
+        if (blocks_[i].free) {
+            blocks_[i].free = false;
+            blocks_[i].ref_count = 1;
+            return i;
+        }
+    }
+    return -1;
+}
+
+void BlockPool::zero_block(int32_t id) {
+    hipStream_t s = static_cast<hipStream_t>(stream_);
+    check(hipMemsetAsync(k_ + (int64_t)id * block_bytes_, 0, block_bytes_, s), "zero block K");
+    check(hipMemsetAsync(v_ + (int64_t)id * block_bytes_, 0, block_bytes_, s), "zero block V");
+    if (k_scale_) {
+        const size_t n = sizeof(uint16_t) * scale_layer_ * num_layers_;
+        check(hipMemsetAsync(k_scale_ + (int64_t)id * scale_layer_ * num_layers_, 0, n, s), "zero scales");
+        check(hipMemsetAsync(v_scale_ + (int64_t)id * scale_layer_ * num_layers_, 0, n, s), "zero scales");
+    }
+}
+
+void BlockPool::free(int32_t block_id) {
+    std::lock_guard<std::mutex> lock(mtx_);
+    if (block_id < 0 || (size_t)block_id >= blocks_.size()) return;
+    KVsBlock& b = blocks_[block_id];
+    b.ref_count--;
+    if (b.ref_count <= 0) {
+        b.ref_count = 0;
+        b.free = true;
+        zero_block(block_id);  // the reference clears a freed block's data
+    }
+}
+
+void BlockPool::ref(int32_t block_id) {
+    std::lock_guard<std::mutex> lock(mtx_);
+    if (block_id < 0 || (size_t)block_id >= blocks_.size()) return;
+    blocks_[block_id].ref_count++;
+}
+
+void BlockPool::deref(int32_t block_id) {
+    std::lock_guard<std::mutex> lock(mtx_);
+    if (block_id < 0 || (size_t)block_id >= blocks_.size()) return;
+    KVsBlock& b = blocks_[block_id];
+    b.ref_count--;
+    if (b.ref_count <= 0) {
+        b.ref_count = 0;
+        b.free = true;
+    }
+}
+
+uint8_t* BlockPool::get_k_raw(int32_t block_id, int32_t layer) {
+    if (block_id < 0 || (size_t)block_id >= blocks_.size() || layer < 0 || layer >= num_layers_)
+        return nullptr;
+    return k_ + (int64_t)block_id * block_bytes_ + (int64_t)layer * layer_bytes_;
+}
+
+uint8_t* BlockPool::get_v_raw(int32_t block_id, int32_t layer) {
+    if (block_id < 0 || (size_t)block_id >= blocks_.size() || layer < 0 || layer >= num_layers_)
+        return nullptr;
+    return v_ + (int64_t)block_id * block_bytes_ + (int64_t)layer * layer_bytes_;
+}
+
+const uint8_t* BlockPool::get_k_raw(int32_t block_id, int32_t layer) const {
+    return const_cast<BlockPool*>(this)->get_k_raw(block_id, layer);
+}
+
+const uint8_t* BlockPool::get_v_raw(int32_t block_id, int32_t layer) const {
+    return const_cast<BlockPool*>(this)->get_v_raw(block_id, layer);
+}
+
+uint16_t* BlockPool::get_k_scale_raw(int32_t block_id, int32_t layer) const {
+    if (!k_scale_ || block_id < 0 || (size_t)block_id >= blocks_.size() || layer < 0 ||
+        layer >= num_layers_)
+        return nullptr;
+    return k_scale_ + ((int64_t)block_id * num_layers_ + layer) * scale_layer_;
+}
+
+uint16_t* BlockPool::get_v_scale_raw(int32_t block_id, int32_t layer) const {
+    if (!v_scale_ || block_id < 0 || (size_t)block_id >= blocks_.size() || layer < 0 ||
+        layer >= num_layers_)
+        return nullptr;
+    return v_scale_ + ((int64_t)block_id * num_layers_ + layer) * scale_layer_;
+}
+
+float* BlockPool::get_k(int32_t block_id, int32_t layer) {
+    const uint8_t* raw = get_k_raw(block_id, layer);
+    if (!raw) return nullptr;
+    std::vector<uint8_t> host((size_t)layer_bytes_);
+    std::vector<uint16_t> sc((size_t)scale_layer_);
+    std::lock_guard<std::mutex> lock(mtx_);
+    hipStream_t s = static_cast<hipStream_t>(stream_);
+    check(hipStreamSynchronize(s), "get_k sync");
+    check(hipMemcpy(host.data(), raw, layer_bytes_, hipMemcpyDeviceToHost), "get_k copy");
+    if (k_scale_)
+        check(hipMemcpy(sc.data(), get_k_scale_raw(block_id, layer), sizeof(uint16_t) * scale_layer_,
+                        hipMemcpyDeviceToHost), "get_k scales");
+    decode_rows(host.data(), sc.data(), k_convert_buf_.data(), kv_dim_, head_dim_, kv_dtype_);
+    return k_convert_buf_.data();
+}
+
+float* BlockPool::get_v(int32_t block_id, int32_t layer) {
+    const uint8_t* raw = get_v_raw(block_id, layer);
+    if (!raw) return nullptr;
+    std::vector<uint8_t> host((size_t)layer_bytes_);
+    std::vector<uint16_t> sc((size_t)scale_layer_);
+    std::lock_guard<std::mutex> lock(mtx_);
+    hipStream_t s = static_cast<hipStream_t>(stream_);
+    check(hipStreamSynchronize(s), "get_v sync");
+    check(hipMemcpy(host.data(), raw, layer_bytes_, hipMemcpyDeviceToHost), "get_v copy");
+    if (v_scale_)
+        check(hipMemcpy(sc.data(), get_v_scale_raw(block_id, layer), sizeof(uint16_t) * scale_layer_,
+                        hipMemcpyDeviceToHost), "get_v scales");
+    decode_rows(host.data(), sc.data(), v_convert_buf_.data(), kv_dim_, head_dim_, kv_dtype_);
+    return v_convert_buf_.data();
+}
+
+const float* BlockPool::get_k(int32_t block_id, int32_t layer) const {
+    return const_cast<BlockPool*>(this)->get_k(block_id, layer);
+}
+
+const float* BlockPool::get_v(int32_t block_id, int32_t layer) const {
+    return const_cast<BlockPool*>(this)->get_v(block_id, layer);
+}
+
+void BlockPool::copy_to(int32_t dst, int32_t src) {
+    std::lock_guard<std::mutex> lock(mtx_);
+    if (dst < 0 || dst >= (int32_t)blocks_.size()) return;
+    if (src < 0 || src >= (int32_t)blocks_.size()) return;
+    hipStream_t s = static_cast<hipStream_t>(stream_);
+    check(hipMemcpyAsync(k_ + (int64_t)dst * block_bytes_, k_ + (int64_t)src * block_bytes_,
+                         block_bytes_, hipMemcpyDeviceToDevice, s), "copy_to K");
+    check(hipMemcpyAsync(v_ + (int64_t)dst * block_bytes_, v_ + (int64_t)src * block_bytes_,
+                         block_bytes_, hipMemcpyDeviceToDevice, s), "copy_to V");
+    if (k_scale_) {
+        const int64_t n = scale_layer_ * num_layers_;
+        check(hipMemcpyAsync(k_scale_ + dst * n, k_scale_ + src * n, sizeof(uint16_t) * n,
+                             hipMemcpyDeviceToDevice, s), "copy_to K scales");
+        check(hipMemcpyAsync(v_scale_ + dst * n, v_scale_ + src * n, sizeof(uint16_t) * n,
+                             hipMemcpyDeviceToDevice, s), "copy_to V scales");
+    }
+}
+
+int32_t BlockPool::free_count() const {
+    int32_t c = 0;
+    for (const auto& b : blocks_) c += b.free ? 1 : 0;
+    return c;
+}
+
+int32_t BlockPool::used_count() const { return (int32_t)blocks_.size() - free_count(); }
+
+void BlockPool::reset() {
+    std::lock_guard<std::mutex> lock(mtx_);
+    for (auto& b : blocks_) {
+        b.ref_count = 0;
+        b.free = true;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream_);
+    const size_t nb = std::max<size_t>(blocks_.size(), 1);
+    check(hipMemsetAsync(k_, 0, (size_t)block_bytes_ * nb, s), "reset K");
+    check(hipMemsetAsync(v_, 0, (size_t)block_bytes_ * nb, s), "reset V");
+    if (k_scale_) {
+        const size_t n = sizeof(uint16_t) * scale_layer_ * num_layers_ * nb;
+        check(hipMemsetAsync(k_scale_, 0, n, s), "reset K scales");
+        check(hipMemsetAsync(v_scale_, 0, n, s), "reset V scales");
+    }
+}
+
+KVsBlock& BlockPool::get_block(int32_t block_id) { return blocks_[block_id]; }
+
+const KVsBlock& BlockPool::get_block(int32_t block_id) const { return blocks_[block_id]; }
+
+vcpp_kv_pages BlockPool::pages(int32_t layer) const {
+    vcpp_kv_pages p{};
+    p.dtype = kv_dtype_ == KVDtype::FP32 ? VCPP_KV_F32 : kv_dtype_ == KVDtype::FP16 ? VCPP_KV_F16 : VCPP_KV_I8;
+    p.block_size = BLOCK_SIZE;
+    p.num_kv_heads = kv_dim_ / head_dim_;
+    p.head_dim = head_dim_;
+    p.num_blocks = (int64_t)blocks_.size();
+    p.block_stride = block_bytes_ / kv_elem_size(kv_dtype_);
+    p.scale_block_stride = scale_layer_ * num_layers_;
+    p.k = k_ + (int64_t)layer * layer_bytes_;
+    p.v = v_ + (int64_t)layer * layer_bytes_;
+    p.k_scale = k_scale_ ? k_scale_ + (int64_t)layer * scale_layer_ : nullptr;
+    p.v_scale = v_scale_ ? v_scale_ + (int64_t)layer * scale_layer_ : nullptr;
+    return p;
+}
+
+// ---- KVCacheManager ---------------------------------------------------------
+
+KVCacheManager::KVCacheManager(int32_t num_layers, int32_t kv_dim, int32_t num_blocks,
+                               KVDtype kv_dtype, int32_t head_dim)
+    : pool_(num_blocks, num_layers, kv_dim, kv_dtype, head_dim) {}
+
+KVCacheManager::~KVCacheManager() {}
+
+bool KVCacheManager::alloc_blocks(int32_t num_blocks, std::vector<int32_t>& out) {
+    out.clear();
+    out.reserve(num_blocks);
+    for (int32_t i = 0; i < num_blocks; ++i) {
+        const int32_t bid = pool_.alloc();
+        if (bid < 0) return false;
+        out.push_back(bid);
+    }
+    return true;
+}
+
+void KVCacheManager::free_blocks(const std::vector<int32_t>& blocks_to_free) {
+    for (int32_t bid : blocks_to_free) pool_.free(bid);
+}
+
+void KVCacheManager::copy_blocks(const std::vector<int32_t>& src, const std::vector<int32_t>& dst) {
+    for (size_t i = 0; i < src.size() && i < dst.size(); ++i) pool_.copy_to(dst[i], src[i]);
+}
+
+void write_kv_rows(KVCacheManager& m, int32_t layer, const std::vector<int64_t>& slots,
+                   const float* k_data, const float* v_data);  // paged_attention.cpp
+
+void KVCacheManager::write_kv(int32_t block_id, int32_t layer, int32_t pos_in_block,
+                              const float* k_data, const float* v_data, int32_t kv_dim) {
+    if (pos_in_block < 0 || pos_in_block >= BLOCK_SIZE) return;
+    if (!pool_.get_k_raw(block_id, layer) || kv_dim != pool_.kv_dim()) return;
+    write_kv_rows(*this, layer, {(int64_t)block_id * BLOCK_SIZE + pos_in_block}, k_data, v_data);
+}
+
+void KVCacheManager::read_kv(int32_t block_id, int32_t layer, int32_t pos_in_block,
+                             float* k_data, float* v_data, int32_t kv_dim) const {
+    if (pos_in_block < 0 || pos_in_block >= BLOCK_SIZE) return;
+    if (!pool_.get_k_raw(block_id, layer) || kv_dim != pool_.kv_dim()) return;
+    const float* k = pool_.get_k(block_id, layer);
+    std::memcpy(k_data, k + (int64_t)pos_in_block * kv_dim, sizeof(float) * kv_dim);
+    const float* v = pool_.get_v(block_id, layer);
+    std::memcpy(v_data, v + (int64_t)pos_in_block * kv_dim, sizeof(float) * kv_dim);
+}
+
+int32_t KVCacheManager::free_blocks_count() const { return pool_.free_count(); }
+
+int32_t KVCacheManager::used_blocks_count() const { return pool_.used_count(); }
