@@ -111,6 +111,10 @@ void orc_quant_i8(const float* x, int32_t d, int8_t* q, uint16_t* scale) {
     }
 }
 
+void orc_quant_i8_rows(const float* x, int64_t rows, int32_t d, int8_t* q, uint16_t* scales) {
+    for (int64_t r = 0; r < rows; r++) orc_quant_i8(x + r * d, d, q + r * d, scales + r);
+}
+
 /* ---- pool access ------------------------------------------------------- */
 
 /* Mirrors BlockPool::get_k/get_v returning NULL for an out-of-range block id

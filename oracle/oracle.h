@@ -51,6 +51,8 @@ void orc_f16_decode_n(const uint16_t* h, float* x, int64_t n);
  * a zero vector gets scale 0 and q = 0.  Build definition (the reference has no
  * INT8 KV; src/config.h:69-73). */
 void orc_quant_i8(const float* x, int32_t d, int8_t* q, uint16_t* scale);
+/* orc_quant_i8 over `rows` consecutive rows of d values. */
+void orc_quant_i8_rows(const float* x, int64_t rows, int32_t d, int8_t* q, uint16_t* scales);
 uint16_t orc_f16_encode_rne(float x);
 
 /* Single-query paged attention, reference src/paged_attention.cpp:11-90.

@@ -56,6 +56,7 @@ def orc():
         L.orc_f16_encode_trunc_n.argtypes = [vp, vp, i64]
         L.orc_f16_decode_n.argtypes = [vp, vp, i64]
         L.orc_quant_i8.argtypes = [vp, i32, vp, vp]
+        L.orc_quant_i8_rows.argtypes = [vp, i64, i32, vp, vp]
         L.orc_paged_attention.argtypes = [ctypes.POINTER(OrcPool), vp, vp, i32, i32, i32, vp]
         L.orc_decode_batch.argtypes = [ctypes.POINTER(OrcPool), vp, vp, i64, vp, vp, i32, i32,
                                        vp, i32]
@@ -134,9 +135,7 @@ def quant_i8(x):
     rows = x.reshape(-1, D)
     q = np.empty(rows.shape, dtype=np.int8)
     s = np.empty(rows.shape[0], dtype=np.uint16)
-    L = orc()
-    for i in range(rows.shape[0]):
-        L.orc_quant_i8(_p(rows[i]), D, _p(q[i]), _p(s[i:i + 1]))
+    orc().orc_quant_i8_rows(_p(rows), rows.shape[0], D, _p(q), _p(s))
     return q.reshape(x.shape), s.reshape(x.shape[:-1])
 
 
