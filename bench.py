@@ -43,6 +43,11 @@ def parse():
                     help="split-K partition size (0 = library default)")
     ap.add_argument("--prefill-steps", type=int, default=20)
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill leg")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the config 4 (long context) and config 5 (int8 mixed) legs")
+    ap.add_argument("--config-steps", type=int, default=20)
+    ap.add_argument("--only", choices=["decode", "prefill", "config4", "config5"],
+                    help="run one leg only and print its JSON (for profiling)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the prefill leg (for profiling its kernel)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -162,6 +167,145 @@ def bench_prefill(torch, pyvcpp, args):
 
 
 # ---------------------------------------------------------------------------
+# config 4: long-context decode; config 5: int8 mixed decode + prefill step
+
+def timed(torch, fn, steps, warmup=3):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def random_tables(torch, g, lens, nb, dev):
+    nblk = [(int(c) + BS - 1) // BS for c in lens]
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    t = torch.full((len(lens), max(nblk)), -1, dtype=torch.int32)
+    off = 0
+    for i, n in enumerate(nblk):
+        t[i, :n] = perm[off:off + n]
+        off += n
+    return t.to(dev), nblk
+
+
+def bench_config4(torch, pyvcpp, args):
+    """16 sequences x 32768 tokens, fp16 pages scattered over a pool of 1.25x
+    the tokens, split-K over 256-token partitions (the config's statement) and
+    the balanced split (the default); 3 rotating pools."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(args.seed + 40)
+    gd = torch.Generator(device=dev).manual_seed(args.seed + 41)
+    ctx = torch.full((16,), 32768, dtype=torch.int32)
+    nb = int(1.25 * int(ctx.sum()) / BS)
+    sets = []
+    for _ in range(3):
+        k = torch.randn((nb, BS, HKV, D), generator=gd, device=dev, dtype=torch.float16)
+        v = torch.randn((nb, BS, HKV, D), generator=gd, device=dev, dtype=torch.float16)
+        tables, nblk = random_tables(torch, g, ctx.tolist(), nb, dev)
+        sets.append((pyvcpp.kv_pages(pyvcpp.KV_F16, k, v, BS, HKV, D, nb, BS * HKV * D), k, v, tables))
+    q = torch.randn((16, H, D), generator=gd, device=dev)
+    out = torch.empty_like(q)
+    ctx_d = ctx.to(dev)
+    nbytes = int(ctx.sum()) * 2 * HKV * D * 2 + 16 * H * D * 8 + sum(nblk) * 4
+    res = {}
+    for part in (256, 0):
+        need = pyvcpp.decode_workspace_size(sets[0][0], 16, H, 32768, part)
+        ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=dev)
+        i = [0]
+
+        def step():
+            pg, _, _, tb = sets[i[0] % 3]
+            i[0] += 1
+            pyvcpp.paged_decode(pg, q, out, tb, ctx_d, 32768, H, partition_size=part, workspace=ws)
+        dt = timed(torch, step, args.config_steps)
+        pyvcpp.profile_enable(True)
+        for _ in range(args.config_steps):
+            step()
+        torch.cuda.synchronize()
+        kms, kn = pyvcpp.profile_read(pyvcpp.KERNEL_DECODE)
+        mms, mn = pyvcpp.profile_read(pyvcpp.KERNEL_MERGE)
+        pyvcpp.profile_enable(False)
+        ks = kms / max(kn, 1) / 1e3
+        res["partition_%d" % part if part else "balanced"] = {
+            "ms_per_step": round(dt * 1e3, 4), "TB/s": round(nbytes / dt / 1e12, 4),
+            "pct_of_hbm_peak": round(100 * nbytes / dt / 1e12 / HBM_PEAK_TBS, 2),
+            "decode_kernel_us": round(ks * 1e6, 1), "merge_kernel_us": round(mms / max(mn, 1) * 1e3, 1),
+            "kernel_TB/s": round(nbytes / ks / 1e12, 4)}
+    return {"metric": "long-context decode HBM TB/s", "unit": "TB/s",
+            "config": {"workload": "BASELINE config 4: 16 seqs x 32768 ctx, 64 q / 8 kv heads, "
+                                   "head_dim 80, fp16 pages scattered over a 1.25x pool",
+                       "bytes_per_step": nbytes},
+            "value": res["balanced"]["TB/s"], "variants": res, "steps": args.config_steps}
+
+
+def bench_config5(torch, pyvcpp, args):
+    """128 decode sequences (ctx U[1024, 8192]) + 4 prefill chunks of 512 new
+    tokens on 1024-token prefixes in one step, int8 pages with fp16 scales
+    (quantised on the device by vcpp_write_kv from N(0,1) values)."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(args.seed + 50)
+    gd = torch.Generator(device=dev).manual_seed(args.seed + 51)
+    dctx = torch.randint(1024, 8193, (128,), generator=g, dtype=torch.int32)
+    plen = [1024 + 512] * 4
+    lens = dctx.tolist() + plen
+    nb = math.ceil(1.25 * sum(lens) / BS)
+    k8 = torch.empty((nb, BS, HKV, D), dtype=torch.int8, device=dev)
+    v8 = torch.empty_like(k8)
+    ks = torch.zeros((nb, HKV, BS), dtype=torch.int16, device=dev)
+    vs = torch.zeros_like(ks)
+    pages = pyvcpp.kv_pages(pyvcpp.KV_I8, k8, v8, BS, HKV, D, nb, BS * HKV * D, ks, vs, HKV * BS)
+    chunk = 1 << 16  # fill every slot from fp32 N(0,1) through the device quantiser
+    for s0 in range(0, nb * BS, chunk):
+        n = min(chunk, nb * BS - s0)
+        kf = torch.randn((n, HKV, D), generator=gd, device=dev)
+        vf = torch.randn((n, HKV, D), generator=gd, device=dev)
+        slots = torch.arange(s0, s0 + n, dtype=torch.int64, device=dev)
+        pyvcpp.write_kv(pages, kf, vf, slots)
+    tables, nblk = random_tables(torch, g, lens, nb, dev)
+    dtab, ptab = tables[:128].contiguous(), tables[128:].contiguous()
+    qd = torch.randn((128, H, D), generator=gd, device=dev)
+    od = torch.empty_like(qd)
+    qp = torch.randn((4 * 512, H, D), generator=gd, device=dev).half()
+    op = torch.empty((4 * 512, H, D), dtype=torch.float32, device=dev)
+    q_start = torch.arange(0, 4 * 512 + 1, 512, dtype=torch.int32, device=dev)
+    prefix = torch.full((4,), 1024, dtype=torch.int32, device=dev)
+    dctx_d = dctx.to(dev)
+    need = pyvcpp.decode_workspace_size(pages, 128, H, 8192, 0)
+    ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=dev)
+
+    def step():
+        pyvcpp.paged_decode(pages, qd, od, dtab, dctx_d, 8192, H, workspace=ws)
+        pyvcpp.paged_prefill(pages, qp.view(torch.int16), op, ptab, q_start, prefix, 512, H)
+    dt = timed(torch, step, args.config_steps)
+    pyvcpp.profile_enable(True)
+    for _ in range(args.config_steps):
+        step()
+    torch.cuda.synchronize()
+    times = {name: pyvcpp.profile_read(kid) for name, kid in
+             (("decode", pyvcpp.KERNEL_DECODE), ("merge", pyvcpp.KERNEL_MERGE),
+              ("prefill", pyvcpp.KERNEL_PREFILL))}
+    pyvcpp.profile_enable(False)
+    dbytes = (int(dctx.sum()) * (2 * HKV * D + 2 * HKV * 2) + 128 * H * D * 8
+              + sum(nblk[:128]) * 4)
+    pairs = 4 * sum(1024 + i + 1 for i in range(512))
+    flops = 4 * D * H * pairs
+    t_star = max(dbytes / (HBM_PEAK_TBS * 1e12), flops / (F16_MFMA_PEAK_TFS * 1e12))
+    us = {k: round(v[0] / max(v[1], 1) * 1e3, 1) for k, v in times.items()}
+    return {"metric": "int8 mixed step: fraction of T* = max(bytes/8 TB/s, flops/2.5 PF)",
+            "value": round(t_star / dt, 4), "unit": "fraction",
+            "ms_per_step": round(dt * 1e3, 4), "t_star_ms": round(t_star * 1e3, 4),
+            "decode_TB/s_in_kernel": round(dbytes / (us["decode"] * 1e-6) / 1e12, 3),
+            "prefill_TFLOP/s_in_kernel": round(flops / (us["prefill"] * 1e-6) / 1e12, 1),
+            "kernel_us": us, "steps": args.config_steps,
+            "config": {"workload": "BASELINE config 5: 128 decode seqs ctx U[1024,8192] + 4 prefill "
+                                   "chunks x 512 on 1024-token prefixes, int8 KV + fp16 scales, GQA 8:1, "
+                                   "head_dim 80", "decode_bytes": dbytes, "prefill_flops": flops}}
+
+
+# ---------------------------------------------------------------------------
 # CPU baseline: the reference's own paged_attention() (oracle/_ref, built
 # from the reference sources), single-threaded, over a bounded sample of the
 # same batch (an FP32 pool holding the decoded fp16 values: identical math).
@@ -233,8 +377,14 @@ def main():
         print(json.dumps({"copy_bytes_read": x.numel() * 2, "copy_bytes_written": y.numel() * 2,
                           "launches": 5}))
         return
-    if args.prefill_only:
+    if args.prefill_only or args.only == "prefill":
         print(json.dumps(bench_prefill(torch, pyvcpp, args)))
+        return
+    if args.only == "config4":
+        print(json.dumps(bench_config4(torch, pyvcpp, args)))
+        return
+    if args.only == "config5":
+        print(json.dumps(bench_config5(torch, pyvcpp, args)))
         return
 
     w = decode_workload(torch, args.seed)
@@ -288,8 +438,13 @@ def main():
                      "merge_avg_us": round(mrg_ms / max(mrg_n, 1) * 1e3, 2)},
         "prefill": None,
     }
+    if args.only == "decode":
+        args.no_prefill = args.no_configs = args.no_cpu = True
     if not args.no_prefill:
         result["prefill"] = bench_prefill(torch, pyvcpp, args)
+    if not args.no_configs:
+        result["config4"] = bench_config4(torch, pyvcpp, args)
+        result["config5"] = bench_config5(torch, pyvcpp, args)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(torch, w, args.cpu_seconds)
     else:
