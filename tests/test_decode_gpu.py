@@ -48,9 +48,10 @@ def test_config1(cuda, kind, partition):
     assert_close(got, want, *TOL[kind], what="config1 kind=%d P=%d" % (kind, partition))
 
 
+@pytest.mark.parametrize("partition", [64, 0])
 @pytest.mark.parametrize("kind", [O.ORC_F32, O.ORC_F16, O.ORC_I8])
-@pytest.mark.parametrize("heads", [(1, 1), (8, 1), (64, 8), (12, 4), (32, 2)])
-def test_small_cases(cuda, kind, heads):
+@pytest.mark.parametrize("heads", [(1, 1), (8, 1), (64, 8), (12, 4), (32, 2), (32, 8)])
+def test_small_cases(cuda, kind, heads, partition):
     H, Hkv = heads
     ctx = np.array([0, 1, 15, 16, 17, 33, 100, 257], dtype=np.int32)
     nb = 64
@@ -58,24 +59,26 @@ def test_small_cases(cuda, kind, heads):
     q = O.normal(13 + H, (len(ctx), H, 80))
     tables = random_tables(17, ctx, nb)
     want = O.decode(pool, q, tables, ctx, H)
-    got = gpu_decode(DevPool(pool), q, tables, ctx, H, partition_size=64)
-    assert_close(got, want, *TOL[kind], what="small H=%d Hkv=%d kind=%d" % (H, Hkv, kind))
+    got = gpu_decode(DevPool(pool), q, tables, ctx, H, partition_size=partition)
+    assert_close(got, want, *TOL[kind], what="small H=%d Hkv=%d kind=%d P=%d" % (H, Hkv, kind, partition))
     assert np.all(got[0] == 0.0), "ctx=0 must give zeros"
 
 
+@pytest.mark.parametrize("partition", [128, 0])
 @pytest.mark.parametrize("D", [64, 128])
-def test_other_head_dims(cuda, D):
+def test_other_head_dims(cuda, D, partition):
     ctx = np.array([5, 48, 300], dtype=np.int32)
     pool = O.make_pool(O.ORC_F16, 21, 40, 8, D)
     q = O.normal(23, (3, 64, D))
     tables = random_tables(29, ctx, 40)
     want = O.decode(pool, q, tables, ctx, 64)
-    got = gpu_decode(DevPool(pool), q, tables, ctx, 64, partition_size=128)
-    assert_close(got, want, *TOL[O.ORC_F16], what="D=%d" % D)
+    got = gpu_decode(DevPool(pool), q, tables, ctx, 64, partition_size=partition)
+    assert_close(got, want, *TOL[O.ORC_F16], what="D=%d P=%d" % (D, partition))
 
 
+@pytest.mark.parametrize("partition", [64, 0])
 @pytest.mark.parametrize("kind", [O.ORC_F32, O.ORC_F16, O.ORC_I8])
-def test_skip_rules(cuda, kind):
+def test_skip_rules(cuda, kind, partition):
     """Invalid block ids and positions past the table are skipped, as the
     reference does (src/paged_attention.cpp:38,42)."""
     nb = 48
@@ -88,8 +91,8 @@ def test_skip_rules(cuda, kind):
     table_lens = np.array([13, 13, 6, 2], dtype=np.int32)  # row 2/3 shorter than ctx
     want = O.decode(pool, q, tables, ctx, 64, table_lens=table_lens)
     got = gpu_decode(DevPool(pool), q, tables, ctx, 64, table_lens=table_lens,
-                     partition_size=64)
-    assert_close(got, want, *TOL[kind], what="skip rules kind=%d" % kind)
+                     partition_size=partition)
+    assert_close(got, want, *TOL[kind], what="skip rules kind=%d P=%d" % (kind, partition))
 
 
 def test_all_positions_skipped_gives_zero(cuda):
@@ -176,3 +179,43 @@ def test_workspace_reuse(cuda, partition):
                             partition_size=partition, workspace=ws)
         torch.cuda.synchronize()
         assert_close(out.cpu().numpy(), want, *TOL[O.ORC_F16], what="reuse it=%d" % it)
+
+
+def test_many_short_sequences(cuda):
+    """Hundreds of short, ragged sequences (many per workgroup range, several
+    empty): the balanced split switches sequence inside ranges constantly."""
+    rng = np.random.default_rng(3)
+    ctx = rng.integers(0, 70, 700).astype(np.int32)
+    ctx[::37] = 0
+    nb = int(sum((c + 15) // 16 for c in ctx)) + 16
+    pool = O.make_pool(O.ORC_F16, 211, nb, 8, 80)
+    q = O.normal(212, (len(ctx), 64, 80))
+    tables = random_tables(213, ctx, nb)
+    want = O.decode(pool, q, tables, ctx, 64)
+    got = gpu_decode(DevPool(pool), q, tables, ctx, 64)
+    assert_close(got, want, *TOL[O.ORC_F16], what="many short")
+    assert np.all(got[ctx == 0] == 0.0)
+
+
+def test_block_size_32(cuda):
+    """Pages of 32 tokens: a 16-token tile is half a page."""
+    bs = 32
+    ctx = np.array([1000, 31, 64, 33, 0, 500], dtype=np.int32)
+    nbs = [(c + bs - 1) // bs for c in ctx]
+    nb = sum(nbs) + 5
+    shape = (nb, bs, 8, 80)
+    k = O.f16_trunc(O.normal(221, shape))
+    v = O.f16_trunc(O.normal(222, shape))
+    perm = O.permutation(223, nb)
+    tables = np.full((len(ctx), max(nbs)), -1, np.int32)
+    o = 0
+    for i, n in enumerate(nbs):
+        tables[i, :n] = perm[o:o + n]
+        o += n
+    q = O.normal(224, (len(ctx), 64, 80))
+    pool = O.Pool(O.ORC_F16, k, v, block_size=bs)
+    # the oracle's pool struct carries the block size of its pages
+    want = O.decode(pool, q, tables, ctx, 64)
+    dp = DevPool(pool)
+    got = gpu_decode(dp, q, tables, ctx, 64)
+    assert_close(got, want, *TOL[O.ORC_F16], what="block size 32")

@@ -71,6 +71,7 @@ int device_cus() {
 // Launch geometry and workspace layout of one decode call.
 struct DecodePlan {
     int32_t num_wg = 0;      // fp16/int8: workgroup ranges per kv-head group
+    bool page_mode = false;  // fp16, Hkv 8: page-staged kernel, one workgroup per range
     int32_t partition = 0;   // fp32: tokens per partition
     int32_t max_parts = 0;   // fp32: partitions per sequence
     size_t off_o = 0, off_ml = 0, bytes = 0;
@@ -95,9 +96,15 @@ DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_he
     const int pairs = kv->num_kv_heads * ((group + 7) / 8);
     const int wpw = pairs < 4 ? pairs : 4;
     const int groups = vcpp::decode_group_count(pairs);
-    // Ranges that are all resident at once: 2 waves per SIMD, 4 SIMDs per CU.
+    // The page-staged kernel (balanced split only) unless VCPP_DECODE_PAGE=0.
+    const char* pe = getenv("VCPP_DECODE_PAGE");
+    pl.page_mode = partition_size == 0 && !(pe && pe[0] == '0') &&
+                   vcpp::decode_page_mode_supported(kv->dtype, kv->num_kv_heads, group, D,
+                                                    kv->block_size);
+    // Ranges that are all resident at once: 2 waves per SIMD, 4 SIMDs per CU
+    // (page mode: one 8-wave workgroup per CU covers every kv head).
     const int64_t slots = (int64_t)device_cus() * (8 / wpw);
-    int64_t G = slots / groups;
+    int64_t G = pl.page_mode ? device_cus() : slots / groups;
     const int64_t tiles_upper = (int64_t)num_seqs * ((max_context_len + 15) / 16);
     if (partition_size > 0) {
         G = (tiles_upper * 16 + partition_size - 1) / partition_size;
@@ -238,6 +245,7 @@ int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
     p.partition = pl.partition;
     p.max_parts = pl.max_parts;
     p.num_wg = pl.num_wg;
+    p.page_mode = pl.page_mode ? 1 : 0;
     p.ctx_cap = max_context_len;
     if (need > 0) {
         p.ws_o = reinterpret_cast<float*>(ws + pl.off_o);

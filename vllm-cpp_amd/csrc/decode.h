@@ -48,11 +48,15 @@ struct DecodeParams {
     float2* ws_ml;   // (max in log2 units, sum of exponentials)
     float scale_log2;  // log2(e) / sqrt(head_dim)
     int32_t pipeline;  // fp16/int8 pipeline shape (tuning; 0 = default)
+    int32_t page_mode; // fp16, Hkv 8: one 8-wave workgroup per range staging whole tiles in LDS
 };
 
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);
 // Workgroups along y of the fp16/int8 grid (kv-head groups of up to 4 waves).
 int decode_group_count(int pairs);
 bool decode_head_dim_supported(int kv_dtype, int head_dim);
+// Shapes the page-staged kernel (decode_page_kernel) handles.
+bool decode_page_mode_supported(int kv_dtype, int num_kv_heads, int group, int head_dim,
+                                int block_size);
 
 }  // namespace vcpp

@@ -758,6 +758,357 @@ __global__ __launch_bounds__(256) void merge_parts_kernel(DecodeParams p) {
         if (lane + 64 * k < D) out[lane + 64 * k] = acc[k] * inv;
 }
 
+// ---------------------------------------------------------------------------
+// fp16 pages, Hkv = 8: whole 16-token tiles staged through LDS.
+//
+// One workgroup (8 waves, one per kv head) per CU takes a balanced range of
+// the concatenated tiles.  A tile's K rows (16 tokens x 8 heads x D fp16) and
+// V rows are each one contiguous run in the page, so the workgroup moves them
+// into LDS with global_load_lds_dwordx4 -- every instruction 1 KiB of whole
+// cache lines -- through a ring of kPageStages tiles, one barrier per tile.
+// Within every 16-chunk (256 B) group the chunk order is XOR-swizzled by the
+// group's token (a token row is a whole number of groups when Hkv * D is a
+// multiple of 128), so the K fragment reads (16 tokens of one head) and the
+// transposing V reads hit distinct banks.  Each wave then runs the same MFMA
+// tile step as decode_mfma_kernel on its head and writes complete sequences
+// or (m, l, o) partials for merge_split_kernel.
+
+constexpr int kPageStages = 3;
+constexpr int kPageWaves = 8;      // kv heads per workgroup (Hkv)
+constexpr int kPageWindow = 512;   // tiles listed in LDS at a time
+
+__device__ __attribute__((aligned(16))) const uint32_t kZeroChunk16[4] = {0, 0, 0, 0};
+
+__device__ __forceinline__ void dma16_page(const void* src, uint32_t lds_base) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved) : "s"(lds_base), "v"(src) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// LDS slot of chunk gc (16-byte units) of a tile region whose token rows are
+// RC chunks long: XOR of the low 4 bits with the token.
+__device__ __forceinline__ int page_slot(int gc, int rc) {
+    return (gc & ~15) | ((gc & 15) ^ ((gc / rc) & 15));
+}
+
+struct PageEntry {
+    int bid;     // physical block (-1: zeros)
+    int tok;     // first token of the tile in its block
+    int seq;     // sequence
+    int tis;     // tile index within the sequence
+    int ntiles;  // tiles of the sequence
+    int end;     // usable positions of the sequence
+    int pad0, pad1;
+};
+
+template <int D>
+__global__ __launch_bounds__(kPageWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void decode_page_kernel(DecodeParams p) {
+    constexpr int NC32 = Dims<D>::NC32, NT = Dims<D>::NT;
+    constexpr int HKV = kPageWaves;
+    constexpr int RC = HKV * D / 8;              // chunks per token row (one region)
+    constexpr int REG = 16 * RC * 16;            // bytes of one region (K or V) of a tile
+    constexpr int NI = REG / 1024;               // DMA instructions per region
+    constexpr int PERW = 2 * NI / kPageWaves;    // per wave (K and V)
+    constexpr int STAGE = 2 * REG;
+    static_assert(RC % 16 == 0 && (2 * NI) % kPageWaves == 0, "tile shape");
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    lds_char* lds = reinterpret_cast<lds_char*>((__attribute__((address_space(3))) char*)smem);
+    PageEntry* list = reinterpret_cast<PageEntry*>(smem + kPageStages * STAGE);
+    const uint32_t lds_addr = (uint32_t)(uintptr_t)lds;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int w = blockIdx.x, G = p.num_wg;
+    const int kvh = wave, pair = wave;  // group <= 8: one query chunk per kv head
+    const int head_base = kvh * p.group;
+    const int gc = p.group;
+
+    int T = 0;
+    for (int base = 0; base < p.num_seqs; base += 64)
+        T += wave_sum(base + lane < p.num_seqs ? tiles_of(p, base + lane) : 0);
+    const int a = range_start(w, T, G), b = range_start(w + 1, T, G);
+    const bool zero_owner_tail = (T == 0 && w == 0) || (T > 0 && w == G - 1);
+
+    // Zero the outputs of empty sequences this range owns (wave 0).
+    if (wave == 0) {
+        int carry = 0;
+        for (int base = 0; base < p.num_seqs; base += 64) {
+            const int sl = base + lane;
+            const int nt = sl < p.num_seqs ? tiles_of(p, sl) : 0;
+            const int Sl = carry + wave_excl_scan(nt, lane);
+            carry += wave_sum(nt);
+            const bool zero_here = sl < p.num_seqs && nt == 0 &&
+                                   ((Sl >= a && Sl < b) || (zero_owner_tail && Sl >= T));
+            uint64_t todo = __ballot(zero_here);
+            while (todo) {
+                const int j = __builtin_ctzll(todo);
+                todo &= todo - 1;
+                float* orow = p.out + (int64_t)(base + j) * p.num_heads * D;
+                for (int e = lane; e < p.num_heads * D; e += 64) orow[e] = 0.f;
+            }
+        }
+    }
+
+    // Per-wave DMA lanes: instruction j = wave * PERW + i fills bytes
+    // [1024 j', 1024 j' + 1024) of region j / NI (j' = j mod NI).
+    auto issue = [&](int tau, int win0, int win1) {
+        const uint32_t sbase = lds_addr + (tau % kPageStages) * STAGE;
+        int bid = -1, tok = 0;
+        if (tau < win1) {
+            const PageEntry& e = list[tau - win0];
+            bid = e.bid;
+            tok = e.tok;
+        }
+        const int64_t elem = (int64_t)(bid >= 0 ? bid : 0) * p.block_stride + (int64_t)tok * HKV * D;
+#pragma unroll
+        for (int i = 0; i < PERW; ++i) {
+            const int j = wave * PERW + i;
+            const int which = j >= NI;                 // uniform
+            const int pos = (j - which * NI) * 64 + lane;  // slot in the region
+            const int grp = pos & ~15;
+            const int gcn = grp | ((pos & 15) ^ ((grp / RC) & 15));  // source chunk
+            const char* base = static_cast<const char*>(which ? p.v : p.k);
+            const void* src = bid >= 0 ? (const void*)(base + elem * 2 + (int64_t)gcn * 16)
+                                       : (const void*)kZeroChunk16;
+            dma16_page(src, __builtin_amdgcn_readfirstlane(sbase + which * REG + (j - which * NI) * 1024));
+        }
+    };
+
+    // Fragment state of this wave's head.
+    int cur = -1, first_tis = 0, last_tis = 0, cur_ntiles = 0, cur_end = 0;
+    h8 qa[NC32 > 0 ? NC32 : 1];
+    h4 qr = {};
+    f4 o[NT];
+    float m_run = kMaxSeed, l_run = 0.f;
+
+    auto finalize = [&]() {
+        float lt = l_run;
+        lt += shfl_xor(lt, 16);
+        lt += shfl_xor(lt, 32);
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[t][r] += shfl_xor(o[t][r], 32);
+        float lh[4], mh[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            lh[r] = shfl(lt, (4 * g + r) & 7);
+            mh[r] = shfl(m_run, (4 * g + r) & 7);
+        }
+        const bool complete = first_tis == 0 && last_tis == cur_ntiles - 1;
+        const int slot = first_tis == 0 ? 1 : 0;
+        if (g < 2) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int h = 4 * g + r;
+                if (h >= gc) continue;
+                if (complete) {
+                    const float inv = 1.0f / (lh[r] + 1e-9f);
+                    float* orow = p.out + ((int64_t)cur * p.num_heads + head_base + h) * D;
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) orow[16 * t + c] = o[t][r] * inv;
+                } else {
+                    const int64_t blk = ((int64_t)w * 2 + slot) * p.pairs + pair;
+                    float* orow = p.ws_o + (blk * 8 + h) * D;
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) orow[16 * t + c] = o[t][r];
+                    if (c == 0) p.ws_ml[blk * 16 + h] = make_float2(mh[r], lh[r]);
+                }
+            }
+        }
+    };
+
+    auto start_seq = [&](const PageEntry& e) {
+        cur = e.seq;
+        first_tis = e.tis;
+        cur_ntiles = e.ntiles;
+        cur_end = e.end;
+        const bool qv = (c & 7) < gc;
+        const float* qrow = p.q + ((int64_t)cur * p.num_heads + head_base + (c & 7)) * D;
+#pragma unroll
+        for (int cc = 0; cc < NC32; ++cc) {
+            f4 x0 = {}, x1 = {};
+            if (qv) {
+                x0 = *reinterpret_cast<const f4*>(qrow + 32 * cc + 8 * g);
+                x1 = *reinterpret_cast<const f4*>(qrow + 32 * cc + 8 * g + 4);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float x = i < 4 ? x0[i] : x1[i - 4];
+                const _Float16 hi = (_Float16)x;
+                qa[cc][i] = c < 8 ? hi : (_Float16)(x - (float)hi);
+            }
+        }
+        if constexpr (Dims<D>::REM) {
+            f4 x = {};
+            if (qv) x = *reinterpret_cast<const f4*>(qrow + 32 * NC32 + 4 * g);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const _Float16 hi = (_Float16)x[i];
+                qr[i] = c < 8 ? hi : (_Float16)(x[i] - (float)hi);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) o[t] = f4{0.f, 0.f, 0.f, 0.f};
+        m_run = kMaxSeed;
+        l_run = 0.f;
+    };
+
+    // LDS byte offsets of this lane's K fragments (token c, head kvh) and V
+    // reads (tokens 4g + c/4 [+ 0..3 via the transpose], dims 16t + 4(c&3)).
+    auto kofs = [&](int chunk) { return page_slot(c * RC + kvh * (D / 8) + chunk, RC) * 16; };
+    auto vofs = [&](int t) {
+        const int tok = 4 * g + (c >> 2);
+        const int dim = 16 * t + 4 * (c & 3);
+        return REG + page_slot(tok * RC + kvh * (D / 8) + dim / 8, RC) * 16 + (dim & 7) * 2;
+    };
+
+    auto compute_tile = [&](int tau, const PageEntry& e) {
+        lds_char* sb = lds + (tau % kPageStages) * STAGE;
+        const int pos0 = e.tis * kTile;
+        const bool full = e.bid >= 0 && pos0 + kTile <= cur_end;  // uniform
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int cc = 0; cc < NC32; ++cc) {
+            const h8 kf = *reinterpret_cast<__attribute__((address_space(3))) h8*>(sb + kofs(4 * cc + g));
+            acc = mfma32(kf, qa[cc], acc);
+        }
+        if constexpr (Dims<D>::REM) {
+            const h4 kf = *reinterpret_cast<__attribute__((address_space(3))) h4*>(
+                sb + kofs(4 * NC32 + (g >> 1)) + (g & 1) * 8);
+            const f4 zero = {0.f, 0.f, 0.f, 0.f};
+            acc += mfma16(kf, qr, zero);
+        }
+        float sc[4];
+        float mx = kMaxSeed;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float x = (acc[r] + dpp_ror8(acc[r])) * p.scale_log2;
+            if (!full) x = (e.bid >= 0 && pos0 + 4 * g + r < cur_end) ? x : -__builtin_inff();
+            sc[r] = x;
+            mx = fmaxf(mx, x);
+        }
+        mx = fmaxf(mx, shfl_xor(mx, 16));
+        mx = fmaxf(mx, shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = fast_exp2(m_run - m_new);
+        m_run = m_new;
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float al = shfl(alpha, (4 * g + r) & 7);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) o[t][r] *= al;
+            }
+        }
+        float lsum = 0.f;
+        h4 pa;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float pr = fast_exp2(sc[r] - m_new);
+            lsum += pr;
+            const _Float16 hi = (_Float16)pr;
+            pa[r] = c < 8 ? hi : (_Float16)(pr - (float)hi);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const s4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                reinterpret_cast<__attribute__((address_space(3))) s4*>(sb + vofs(t)));
+            o[t] = mfma16(pa, __builtin_bit_cast(h4, x), o[t]);
+        }
+        l_run = l_run * alpha + lsum;
+    };
+
+    for (int win0 = a; win0 < b; win0 += kPageWindow) {
+        const int win1 = min(b, win0 + kPageWindow);
+        __syncthreads();  // the previous window's list is no longer read
+        // List the window's tiles: every wave scans the sequences; the
+        // workgroup fills the entries of each overlapping one.
+        {
+            int carry = 0;
+            for (int base = 0; base < p.num_seqs; base += 64) {
+                const int sl = base + lane;
+                const int nt = sl < p.num_seqs ? tiles_of(p, sl) : 0;
+                const int Sl = carry + wave_excl_scan(nt, lane);
+                carry += wave_sum(nt);
+                uint64_t todo = __ballot(sl < p.num_seqs && nt > 0 && Sl < win1 && Sl + nt > win0);
+                while (todo) {
+                    const int j = __builtin_ctzll(todo);
+                    todo &= todo - 1;
+                    const int s = base + j;
+                    const int S = __builtin_amdgcn_readlane(Sl, j);
+                    const int n = __builtin_amdgcn_readlane(nt, j);
+                    const int ctx = min(max(p.context_lens[s], 0), p.ctx_cap);
+                    int tlen = p.max_blocks;
+                    if (p.table_lens) tlen = min(tlen, p.table_lens[s]);
+                    const int end = (int)min((int64_t)ctx, (int64_t)tlen * p.block_size);
+                    const int t0 = max(win0, S), t1 = min(win1, S + n);
+                    for (int tt = t0 + tid; tt < t1; tt += kPageWaves * 64) {
+                        const int tis = tt - S;
+                        const int pos = tis * kTile;
+                        const int lb = pos / p.block_size;
+                        int bid = -1;
+                        if (lb < tlen) {
+                            const int id = p.block_tables[(int64_t)s * p.max_blocks + lb];
+                            if (id >= 0 && (int64_t)id < p.num_blocks) bid = id;
+                        }
+                        PageEntry& e = list[tt - win0];
+                        e.bid = bid;
+                        e.tok = pos - lb * p.block_size;
+                        e.seq = s;
+                        e.tis = tis;
+                        e.ntiles = n;
+                        e.end = end;
+                    }
+                }
+                if (carry >= win1) break;
+            }
+        }
+        // Table and length loads land here in a wait the compiler sees (the
+        // DMA ring below is invisible to its counters).
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kPageStages - 1; ++i) issue(win0 + i, win0, win1);
+        for (int tau = win0; tau < win1; ++tau) {
+            wait_vm<(kPageStages - 2) * PERW>();
+            __syncthreads();  // tile tau landed for every wave; tile tau - 1 consumed
+            issue(tau + kPageStages - 1, win0, win1);
+            const PageEntry e = list[tau - win0];
+            if (e.seq != cur) {
+                if (cur >= 0) finalize();
+                start_seq(e);
+            }
+            last_tis = e.tis;
+            compute_tile(tau, e);
+        }
+        wait_vm<0>();
+    }
+    if (cur >= 0) finalize();
+}
+
+template <int D>
+hipError_t launch_page(const DecodeParams& p, hipStream_t stream) {
+    constexpr int STAGE = 2 * 16 * kPageWaves * D * 2;
+    const size_t lds = (size_t)kPageStages * STAGE + kPageWindow * sizeof(PageEntry);
+    static bool attr_set = false;  // one device per process
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute((const void*)decode_page_kernel<D>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(decode_page_kernel<D>, dim3(p.num_wg), dim3(kPageWaves * 64), lds, stream, p);
+    return hipGetLastError();
+}
+
 template <int KV, int D, int TPS, int NBUF>
 hipError_t launch_shape(const DecodeParams& p, hipStream_t stream) {
     const int wpw = p.pairs < kWavesPerGroup ? p.pairs : kWavesPerGroup;
@@ -818,7 +1169,9 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
         case 128: err = launch_mfma<KVT, 128>(p, stream); break;          \
         default: return hipErrorInvalidValue;                             \
     }
-    if (p.kv_dtype == VCPP_KV_F16) {
+    if (p.page_mode) {
+        err = p.head_dim == 64 ? launch_page<64>(p, stream) : launch_page<80>(p, stream);
+    } else if (p.kv_dtype == VCPP_KV_F16) {
         VCPP_DISPATCH_D(VCPP_KV_F16)
     } else {
         VCPP_DISPATCH_D(VCPP_KV_I8)
@@ -836,6 +1189,12 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
     err = hipGetLastError();
     if (prof) prof_end(kKernelMerge, stream);
     return err;
+}
+
+bool decode_page_mode_supported(int kv_dtype, int num_kv_heads, int group, int head_dim,
+                                int block_size) {
+    return kv_dtype == VCPP_KV_F16 && num_kv_heads == kPageWaves && group <= 8 &&
+           (head_dim == 64 || head_dim == 80) && block_size % kTile == 0;
 }
 
 bool decode_head_dim_supported(int kv_dtype, int head_dim) {
