@@ -160,7 +160,7 @@ def bench_prefill(torch, pyvcpp, args):
                    "flop_count": "4*D*H per causal-valid (query, key) pair"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": F16_MFMA_PEAK_TFS,
                      "unit": "TFLOP/s", "frac": round(achieved / F16_MFMA_PEAK_TFS, 4),
-                     "traffic": read_traffic("prefill_mfma_config3_traffic.txt"),
+                     "traffic": read_traffic("prefill_dma_config3_traffic.txt"),
                      "kernel": "prefill_dma_kernel<80>",
                      "kernel_avg_us": round(k_s * 1e6, 1)},
     }
@@ -432,8 +432,8 @@ def main():
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_TBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved * 1e3, 1), "peak": HBM_PEAK_TBS * 1e3,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_TBS, 4),
-                     "traffic": read_traffic("decode_mfma_config2_traffic.txt"),
-                     "kernel": "decode_mfma_kernel<f16,80>",
+                     "traffic": read_traffic("decode_page_config2_traffic.txt"),
+                     "kernel": "decode_page_kernel<80>",
                      "kernel_avg_us": round(dec_avg_s * 1e6, 2),
                      "merge_avg_us": round(mrg_ms / max(mrg_n, 1) * 1e3, 2)},
         "prefill": None,
