@@ -71,7 +71,7 @@ int device_cus() {
 // Launch geometry and workspace layout of one decode call.
 struct DecodePlan {
     int32_t num_wg = 0;      // fp16/int8: workgroup ranges per kv-head group
-    bool page_mode = false;  // fp16, Hkv 8: page-staged kernel, one workgroup per range
+    bool page_mode = false;  // fp16/int8, Hkv 8: page-staged kernel, one workgroup per range
     int32_t partition = 0;   // fp32: tokens per partition
     int32_t max_parts = 0;   // fp32: partitions per sequence
     size_t off_o = 0, off_ml = 0, bytes = 0;
@@ -98,7 +98,15 @@ DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_he
     const int groups = vcpp::decode_group_count(pairs);
     // The page-staged kernel (balanced split only) unless VCPP_DECODE_PAGE=0.
     const char* pe = getenv("VCPP_DECODE_PAGE");
-    pl.page_mode = partition_size == 0 && !(pe && pe[0] == '0') &&
+    // Its 16-byte DMA of int8 pages and scales needs 16-byte aligned bases and
+    // strides (fp16 pages already must be).
+    const bool dma_aligned =
+        kv->dtype != VCPP_KV_I8 ||
+        (kv->block_stride % 16 == 0 && kv->scale_block_stride % 8 == 0 &&
+         reinterpret_cast<uintptr_t>(kv->k) % 16 == 0 && reinterpret_cast<uintptr_t>(kv->v) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(kv->k_scale) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(kv->v_scale) % 16 == 0);
+    pl.page_mode = partition_size == 0 && !(pe && pe[0] == '0') && dma_aligned &&
                    vcpp::decode_page_mode_supported(kv->dtype, kv->num_kv_heads, group, D,
                                                     kv->block_size);
     // Ranges that are all resident at once: 2 waves per SIMD, 4 SIMDs per CU

@@ -48,7 +48,7 @@ struct DecodeParams {
     float2* ws_ml;   // (max in log2 units, sum of exponentials)
     float scale_log2;  // log2(e) / sqrt(head_dim)
     int32_t pipeline;  // fp16/int8 pipeline shape (tuning; 0 = default)
-    int32_t page_mode; // fp16, Hkv 8: one 8-wave workgroup per range staging whole tiles in LDS
+    int32_t page_mode; // fp16/int8, Hkv 8: one 8-wave workgroup per range staging whole tiles in LDS
 };
 
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);

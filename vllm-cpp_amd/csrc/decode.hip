@@ -759,23 +759,60 @@ __global__ __launch_bounds__(256) void merge_parts_kernel(DecodeParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// fp16 pages, Hkv = 8: whole 16-token tiles staged through LDS.
+// fp16 or int8 pages, Hkv = 8: whole 16-token tiles staged through LDS.
 //
 // One workgroup (8 waves, one per kv head) per CU takes a balanced range of
-// the concatenated tiles.  A tile's K rows (16 tokens x 8 heads x D fp16) and
-// V rows are each one contiguous run in the page, so the workgroup moves them
-// into LDS with global_load_lds_dwordx4 -- every instruction 1 KiB of whole
-// cache lines -- through a ring of kPageStages tiles, one barrier per tile.
-// Within every 16-chunk (256 B) group the chunk order is XOR-swizzled by the
-// group's token (a token row is a whole number of groups when Hkv * D is a
-// multiple of 128), so the K fragment reads (16 tokens of one head) and the
-// transposing V reads hit distinct banks.  Each wave then runs the same MFMA
-// tile step as decode_mfma_kernel on its head and writes complete sequences
-// or (m, l, o) partials for merge_split_kernel.
+// the concatenated tiles.  A tile's K rows (16 tokens x 8 heads x D values)
+// and V rows are each one contiguous run in the page, so the workgroup moves
+// them into LDS with global_load_lds_dwordx4 -- every instruction 1 KiB of
+// whole cache lines -- through a ring of tiles, one barrier per tile.  Within
+// every SWZ-chunk group (16-byte chunks; a token row is a whole number of
+// groups) the chunk order is XOR-swizzled by the group's token, so the K
+// fragment reads (16 tokens of one head) and the V reads spread over the
+// banks.  Each wave then runs the MFMA tile step of decode_mfma_kernel on its
+// head and writes complete sequences or (m, l, o) partials for
+// merge_split_kernel.
+//
+// int8 pages: the tile's 8 x 16 K scales and V scales (fp16, [head][token])
+// ride in one more DMA instruction.  K fragments are widened to exact fp16
+// integers in registers and their scale multiplies the fp32 score; each wave
+// widens its head's V rows into a private fp16 tile for the transposing reads,
+// and the V scale multiplies fp32 P before its fp16 split.
 
-constexpr int kPageStages = 3;
 constexpr int kPageWaves = 8;      // kv heads per workgroup (Hkv)
 constexpr int kPageWindow = 512;   // tiles listed in LDS at a time
+
+struct PageEntry {
+    int bid;     // physical block (-1: zeros)
+    int tok;     // first token of the tile in its block
+    int seq;     // sequence
+    int tis;     // tile index within the sequence
+    int ntiles;  // tiles of the sequence
+    int end;     // usable positions of the sequence
+    int pad0, pad1;
+};
+
+template <int KV, int D>
+struct PageCfg {
+    static constexpr bool I8 = KV == VCPP_KV_I8;
+    static constexpr int ES = I8 ? 1 : 2;
+    static constexpr int RC = kPageWaves * D * ES / 16;   // 16-byte chunks per token row
+    static constexpr int HC = D * ES / 16;                // chunks of one head in a row
+    static constexpr int SWZ = RC % 16 == 0 ? 16 : 8;     // swizzle group (chunks)
+    static constexpr int REG = 16 * RC * 16;              // bytes of one region (K or V) of a tile
+    static constexpr int NI = REG / 1024;                 // DMA instructions per region
+    static constexpr int NREAL = 2 * NI + (I8 ? 1 : 0);   // + the scale instruction
+    static constexpr int PERW = (NREAL + kPageWaves - 1) / kPageWaves;
+    static constexpr int STAGE = 2 * REG + (I8 ? 1024 : 0);
+    // int8 tiles carry half the bytes: twice the tiles in flight.
+    static constexpr int STAGES = I8 ? 5 : 3;
+    static constexpr int OFF_JUNK = STAGES * STAGE;       // target of padding DMAs
+    static constexpr int OFF_VT = OFF_JUNK + (PERW * kPageWaves > NREAL ? 1024 : 0);
+    static constexpr int OFF_LIST = OFF_VT + (I8 ? kPageWaves * 16 * D * 2 : 0);
+    static constexpr int LDS = OFF_LIST + kPageWindow * (int)sizeof(PageEntry);
+    static_assert(RC % SWZ == 0 && REG % 1024 == 0 && (D * ES) % 16 == 0, "tile shape");
+    static_assert(LDS <= 160 * 1024, "LDS budget");
+};
 
 __device__ __attribute__((aligned(16))) const uint32_t kZeroChunk16[4] = {0, 0, 0, 0};
 
@@ -792,35 +829,24 @@ __device__ __forceinline__ void wait_vm() {
 }
 
 // LDS slot of chunk gc (16-byte units) of a tile region whose token rows are
-// RC chunks long: XOR of the low 4 bits with the token.
+// rc chunks long: XOR of the low bits (group of SWZ) with the token.
+template <int SWZ>
 __device__ __forceinline__ int page_slot(int gc, int rc) {
-    return (gc & ~15) | ((gc & 15) ^ ((gc / rc) & 15));
+    return (gc & ~(SWZ - 1)) | ((gc & (SWZ - 1)) ^ ((gc / rc) & (SWZ - 1)));
 }
 
-struct PageEntry {
-    int bid;     // physical block (-1: zeros)
-    int tok;     // first token of the tile in its block
-    int seq;     // sequence
-    int tis;     // tile index within the sequence
-    int ntiles;  // tiles of the sequence
-    int end;     // usable positions of the sequence
-    int pad0, pad1;
-};
-
-template <int D>
+template <int KV, int D>
 __global__ __launch_bounds__(kPageWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void decode_page_kernel(DecodeParams p) {
+    using C = PageCfg<KV, D>;
+    constexpr bool I8 = C::I8;
     constexpr int NC32 = Dims<D>::NC32, NT = Dims<D>::NT;
     constexpr int HKV = kPageWaves;
-    constexpr int RC = HKV * D / 8;              // chunks per token row (one region)
-    constexpr int REG = 16 * RC * 16;            // bytes of one region (K or V) of a tile
-    constexpr int NI = REG / 1024;               // DMA instructions per region
-    constexpr int PERW = 2 * NI / kPageWaves;    // per wave (K and V)
-    constexpr int STAGE = 2 * REG;
-    static_assert(RC % 16 == 0 && (2 * NI) % kPageWaves == 0, "tile shape");
+    constexpr int RC = C::RC, HC = C::HC, SWZ = C::SWZ, REG = C::REG, NI = C::NI;
+    constexpr int PERW = C::PERW, STAGE = C::STAGE, STAGES = C::STAGES;
     extern __shared__ __attribute__((aligned(16))) char smem[];
     lds_char* lds = reinterpret_cast<lds_char*>((__attribute__((address_space(3))) char*)smem);
-    PageEntry* list = reinterpret_cast<PageEntry*>(smem + kPageStages * STAGE);
+    PageEntry* list = reinterpret_cast<PageEntry*>(smem + C::OFF_LIST);
     const uint32_t lds_addr = (uint32_t)(uintptr_t)lds;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -857,9 +883,10 @@ void decode_page_kernel(DecodeParams p) {
     }
 
     // Per-wave DMA lanes: instruction j = wave * PERW + i fills bytes
-    // [1024 j', 1024 j' + 1024) of region j / NI (j' = j mod NI).
+    // [1024 j', 1024 j' + 1024) of region j / NI (j' = j mod NI); int8 adds
+    // instruction 2 NI for the scales; the rest pad every wave to PERW.
     auto issue = [&](int tau, int win0, int win1) {
-        const uint32_t sbase = lds_addr + (tau % kPageStages) * STAGE;
+        const uint32_t sbase = lds_addr + (tau % STAGES) * STAGE;
         int bid = -1, tok = 0;
         if (tau < win1) {
             const PageEntry& e = list[tau - win0];
@@ -869,15 +896,27 @@ void decode_page_kernel(DecodeParams p) {
         const int64_t elem = (int64_t)(bid >= 0 ? bid : 0) * p.block_stride + (int64_t)tok * HKV * D;
 #pragma unroll
         for (int i = 0; i < PERW; ++i) {
-            const int j = wave * PERW + i;
-            const int which = j >= NI;                 // uniform
-            const int pos = (j - which * NI) * 64 + lane;  // slot in the region
-            const int grp = pos & ~15;
-            const int gcn = grp | ((pos & 15) ^ ((grp / RC) & 15));  // source chunk
-            const char* base = static_cast<const char*>(which ? p.v : p.k);
-            const void* src = bid >= 0 ? (const void*)(base + elem * 2 + (int64_t)gcn * 16)
-                                       : (const void*)kZeroChunk16;
-            dma16_page(src, __builtin_amdgcn_readfirstlane(sbase + which * REG + (j - which * NI) * 1024));
+            const int j = wave * PERW + i;  // uniform
+            if (j < 2 * NI) {
+                const int which = j >= NI;
+                const int pos = (j - which * NI) * 64 + lane;  // slot in the region
+                const int grp = pos & ~(SWZ - 1);
+                const int gcn = grp | ((pos & (SWZ - 1)) ^ ((grp / RC) & (SWZ - 1)));  // source chunk
+                const char* base = static_cast<const char*>(which ? p.v : p.k);
+                const void* src = bid >= 0 ? (const void*)(base + elem * C::ES + (int64_t)gcn * 16)
+                                           : (const void*)kZeroChunk16;
+                dma16_page(src, __builtin_amdgcn_readfirstlane(sbase + which * REG + (j - which * NI) * 1024));
+            } else if (I8 && j == 2 * NI) {
+                // lanes 0..15: K scales of head lane/2 (32 B = 2 chunks), 16..31: V scales
+                const int head = (lane >> 1) & 7, half = lane & 1;
+                const uint16_t* sp = lane >= 16 ? p.v_scale : p.k_scale;
+                const void* src = bid >= 0 && lane < 32
+                    ? (const void*)(sp + (int64_t)bid * p.scale_block_stride + head * p.block_size + tok + 8 * half)
+                    : (const void*)kZeroChunk16;
+                dma16_page(src, __builtin_amdgcn_readfirstlane(sbase + 2 * REG));
+            } else {
+                dma16_page(kZeroChunk16, lds_addr + C::OFF_JUNK);
+            }
         }
     };
 
@@ -961,36 +1000,75 @@ void decode_page_kernel(DecodeParams p) {
         l_run = 0.f;
     };
 
-    // LDS byte offsets of this lane's K fragments (token c, head kvh) and V
-    // reads (tokens 4g + c/4 [+ 0..3 via the transpose], dims 16t + 4(c&3)).
-    auto kofs = [&](int chunk) { return page_slot(c * RC + kvh * (D / 8) + chunk, RC) * 16; };
+    // LDS byte offset of chunk `chunk` of this lane's token row c, head kvh
+    // (the same in the K and V regions).
+    auto kofs = [&](int chunk) { return page_slot<SWZ>(c * RC + kvh * HC + chunk, RC) * 16; };
+    // fp16: transposing V reads (tokens 4g + c/4 [+ 0..3], dims 16t + 4(c&3)).
     auto vofs = [&](int t) {
         const int tok = 4 * g + (c >> 2);
         const int dim = 16 * t + 4 * (c & 3);
-        return REG + page_slot(tok * RC + kvh * (D / 8) + dim / 8, RC) * 16 + (dim & 7) * 2;
+        return REG + page_slot<SWZ>(tok * RC + kvh * HC + dim / 8, RC) * 16 + (dim & 7) * 2;
     };
+    typedef __attribute__((address_space(3))) uint32_t lds_u32;
+    typedef __attribute__((address_space(3))) i2 lds_i2;
+    lds_char* vt = lds + C::OFF_VT + wave * 16 * D * 2;  // int8: this wave's fp16 V tile
 
     auto compute_tile = [&](int tau, const PageEntry& e) {
-        lds_char* sb = lds + (tau % kPageStages) * STAGE;
+        lds_char* sb = lds + (tau % STAGES) * STAGE;
         const int pos0 = e.tis * kTile;
         const bool full = e.bid >= 0 && pos0 + kTile <= cur_end;  // uniform
         f4 acc = {0.f, 0.f, 0.f, 0.f};
+        i2 ksw = {}, vsw = {};
+        if constexpr (I8) {
+            // K scales of tokens 4g..4g+3 (head kvh), V scales likewise
+            ksw = *reinterpret_cast<lds_i2*>(sb + 2 * REG + kvh * 32 + 8 * g);
+            vsw = *reinterpret_cast<lds_i2*>(sb + 2 * REG + 256 + kvh * 32 + 8 * g);
 #pragma unroll
-        for (int cc = 0; cc < NC32; ++cc) {
-            const h8 kf = *reinterpret_cast<__attribute__((address_space(3))) h8*>(sb + kofs(4 * cc + g));
-            acc = mfma32(kf, qa[cc], acc);
-        }
-        if constexpr (Dims<D>::REM) {
-            const h4 kf = *reinterpret_cast<__attribute__((address_space(3))) h4*>(
-                sb + kofs(4 * NC32 + (g >> 1)) + (g & 1) * 8);
-            const f4 zero = {0.f, 0.f, 0.f, 0.f};
-            acc += mfma16(kf, qr, zero);
+            for (int cc = 0; cc < NC32; ++cc) {
+                const i2 kw = *reinterpret_cast<lds_i2*>(sb + kofs(2 * cc + (g >> 1)) + 8 * (g & 1));
+                acc = mfma32(i8x8_to_h8((uint32_t)kw.x, (uint32_t)kw.y), qa[cc], acc);
+            }
+            if constexpr (Dims<D>::REM) {
+                const uint32_t kw = *reinterpret_cast<lds_u32*>(sb + kofs(2 * NC32) + 4 * g);
+                const f4 zero = {0.f, 0.f, 0.f, 0.f};
+                acc += mfma16(i8x4_to_h4(kw), qr, zero);
+            }
+            // widen V rows of token c into the wave's row-major [16][D] fp16 tile
+#pragma unroll
+            for (int cc = 0; cc < NC32; ++cc) {
+                const i2 vw = *reinterpret_cast<lds_i2*>(sb + REG + kofs(2 * cc + (g >> 1)) + 8 * (g & 1));
+                *reinterpret_cast<__attribute__((address_space(3))) h8*>(vt + (c * D + 32 * cc + 8 * g) * 2) =
+                    i8x8_to_h8((uint32_t)vw.x, (uint32_t)vw.y);
+            }
+            if constexpr (Dims<D>::REM) {
+                const uint32_t vw = *reinterpret_cast<lds_u32*>(sb + REG + kofs(2 * NC32) + 4 * g);
+                *reinterpret_cast<__attribute__((address_space(3))) h4*>(vt + (c * D + 32 * NC32 + 4 * g) * 2) =
+                    i8x4_to_h4(vw);
+            }
+        } else {
+#pragma unroll
+            for (int cc = 0; cc < NC32; ++cc) {
+                const h8 kf = *reinterpret_cast<__attribute__((address_space(3))) h8*>(sb + kofs(4 * cc + g));
+                acc = mfma32(kf, qa[cc], acc);
+            }
+            if constexpr (Dims<D>::REM) {
+                const h4 kf = *reinterpret_cast<__attribute__((address_space(3))) h4*>(
+                    sb + kofs(4 * NC32 + (g >> 1)) + (g & 1) * 8);
+                const f4 zero = {0.f, 0.f, 0.f, 0.f};
+                acc += mfma16(kf, qr, zero);
+            }
         }
         float sc[4];
         float mx = kMaxSeed;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            float x = (acc[r] + dpp_ror8(acc[r])) * p.scale_log2;
+            float x = acc[r] + dpp_ror8(acc[r]);
+            float f = p.scale_log2;
+            if constexpr (I8) {
+                const uint32_t wd = (uint32_t)(r < 2 ? ksw.x : ksw.y);
+                f *= h_to_f((r & 1) ? (wd >> 16) : (wd & 0xFFFFu));
+            }
+            x *= f;
             if (!full) x = (e.bid >= 0 && pos0 + 4 * g + r < cur_end) ? x : -__builtin_inff();
             sc[r] = x;
             mx = fmaxf(mx, x);
@@ -1012,16 +1090,27 @@ void decode_page_kernel(DecodeParams p) {
         h4 pa;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float pr = fast_exp2(sc[r] - m_new);
+            float pr = fast_exp2(sc[r] - m_new);
             lsum += pr;
+            if constexpr (I8) {
+                const uint32_t wd = (uint32_t)(r < 2 ? vsw.x : vsw.y);
+                // masked tokens have pr == 0; the select keeps 0 * garbage out
+                pr = pr > 0.f ? pr * h_to_f((r & 1) ? (wd >> 16) : (wd & 0xFFFFu)) : 0.f;
+            }
             const _Float16 hi = (_Float16)pr;
             pa[r] = c < 8 ? hi : (_Float16)(pr - (float)hi);
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const s4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                reinterpret_cast<__attribute__((address_space(3))) s4*>(sb + vofs(t)));
-            o[t] = mfma16(pa, __builtin_bit_cast(h4, x), o[t]);
+            h4 vf;
+            if constexpr (I8) {
+                vf = read_v_tr<D>(vt, t, g, c);
+            } else {
+                const s4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    reinterpret_cast<__attribute__((address_space(3))) s4*>(sb + vofs(t)));
+                vf = __builtin_bit_cast(h4, x);
+            }
+            o[t] = mfma16(pa, vf, o[t]);
         }
         l_run = l_run * alpha + lsum;
     };
@@ -1076,11 +1165,11 @@ void decode_page_kernel(DecodeParams p) {
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < kPageStages - 1; ++i) issue(win0 + i, win0, win1);
+        for (int i = 0; i < STAGES - 1; ++i) issue(win0 + i, win0, win1);
         for (int tau = win0; tau < win1; ++tau) {
-            wait_vm<(kPageStages - 2) * PERW>();
+            wait_vm<(STAGES - 2) * PERW>();
             __syncthreads();  // tile tau landed for every wave; tile tau - 1 consumed
-            issue(tau + kPageStages - 1, win0, win1);
+            issue(tau + STAGES - 1, win0, win1);
             const PageEntry e = list[tau - win0];
             if (e.seq != cur) {
                 if (cur >= 0) finalize();
@@ -1094,18 +1183,17 @@ void decode_page_kernel(DecodeParams p) {
     if (cur >= 0) finalize();
 }
 
-template <int D>
+template <int KV, int D>
 hipError_t launch_page(const DecodeParams& p, hipStream_t stream) {
-    constexpr int STAGE = 2 * 16 * kPageWaves * D * 2;
-    const size_t lds = (size_t)kPageStages * STAGE + kPageWindow * sizeof(PageEntry);
+    const size_t lds = PageCfg<KV, D>::LDS;
     static bool attr_set = false;  // one device per process
     if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute((const void*)decode_page_kernel<D>,
+        const hipError_t e = hipFuncSetAttribute((const void*)decode_page_kernel<KV, D>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL(decode_page_kernel<D>, dim3(p.num_wg), dim3(kPageWaves * 64), lds, stream, p);
+    hipLaunchKernelGGL((decode_page_kernel<KV, D>), dim3(p.num_wg), dim3(kPageWaves * 64), lds, stream, p);
     return hipGetLastError();
 }
 
@@ -1170,7 +1258,12 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
         default: return hipErrorInvalidValue;                             \
     }
     if (p.page_mode) {
-        err = p.head_dim == 64 ? launch_page<64>(p, stream) : launch_page<80>(p, stream);
+        if (p.kv_dtype == VCPP_KV_I8)
+            err = p.head_dim == 64 ? launch_page<VCPP_KV_I8, 64>(p, stream)
+                                   : launch_page<VCPP_KV_I8, 80>(p, stream);
+        else
+            err = p.head_dim == 64 ? launch_page<VCPP_KV_F16, 64>(p, stream)
+                                   : launch_page<VCPP_KV_F16, 80>(p, stream);
     } else if (p.kv_dtype == VCPP_KV_F16) {
         VCPP_DISPATCH_D(VCPP_KV_F16)
     } else {
@@ -1193,7 +1286,8 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
 
 bool decode_page_mode_supported(int kv_dtype, int num_kv_heads, int group, int head_dim,
                                 int block_size) {
-    return kv_dtype == VCPP_KV_F16 && num_kv_heads == kPageWaves && group <= 8 &&
+    return (kv_dtype == VCPP_KV_F16 || kv_dtype == VCPP_KV_I8) && num_kv_heads == kPageWaves &&
+           group <= 8 &&
            (head_dim == 64 || head_dim == 80) && block_size % kTile == 0;
 }
 
