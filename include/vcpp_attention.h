@@ -165,6 +165,42 @@ int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
 int vcpp_write_kv(const vcpp_kv_pages* kv, const float* k, const float* v, const int64_t* slots,
                   int32_t num_tokens, int32_t fp16_round_nearest, void* stream);
 
+/* ---- v2: query / key preparation (per-head norm, rotary embedding) ------ */
+
+#define VCPP_ROPE_INTERLEAVED 0 /* pairs (2i, 2i+1): the CPU engine, src/paged_engine.cpp:47-62 */
+#define VCPP_ROPE_HALF 1        /* pairs (i, i+head_dim/2): cuda/attention_kernels.cuh:249-287 */
+
+/*
+ * Fused in-place preparation of q and k for attention, one HBM pass:
+ *   q  [num_tokens][num_heads][head_dim] fp32 on the device
+ *   k  [num_tokens][num_kv_heads][head_dim] fp32, or NULL (q only)
+ *   q_norm_weight, k_norm_weight  [head_dim] fp32, or NULL (no norm): per-head
+ *      RMS norm y = (w * x) / sqrt(sum(x^2) / head_dim + eps), the reference
+ *      rms_norm (src/paged_engine.cpp:14-20) applied to each head -- the
+ *      Qwen3 q_norm / k_norm (src/model.h:88-89);
+ *   positions  [num_tokens] int32, or NULL (no rotation): RoPE with
+ *      theta = inv_freq[min(i, inv_freq_size - 1)] * pos for pair i, as
+ *      rope_single (src/paged_engine.cpp:47-62) computes it; style selects the
+ *      pairing (VCPP_ROPE_INTERLEAVED or VCPP_ROPE_HALF).
+ *   inv_freq  [inv_freq_size] fp32 on the device (needed when positions is set)
+ * The norm runs before the rotation (the Qwen3 order).  head_dim even and
+ * <= 256.  Replaces the per-position rope_single calls of the engine
+ * (src/paged_engine.cpp:361-362,377-378,484-485,500-501).
+ */
+int vcpp_qk_norm_rope(float* q, float* k, int32_t num_tokens, int32_t num_heads,
+                      int32_t num_kv_heads, int32_t head_dim, const float* q_norm_weight,
+                      const float* k_norm_weight, float eps, const int32_t* positions,
+                      const float* inv_freq, int32_t inv_freq_size, int32_t style, void* stream);
+
+/* RoPE alone on one tensor x [num_tokens][num_heads][head_dim] (in place). */
+int vcpp_rope(float* x, int32_t num_tokens, int32_t num_heads, int32_t head_dim,
+              const int32_t* positions, const float* inv_freq, int32_t inv_freq_size,
+              int32_t style, void* stream);
+
+/* Per-head RMS norm alone on x [num_rows][head_dim] (in place), weight [head_dim]. */
+int vcpp_head_norm(float* x, const float* weight, float eps, int32_t num_rows, int32_t head_dim,
+                   void* stream);
+
 /* ---- v1: reference launcher signatures (cuda/attention.h) -------------- */
 
 /*
@@ -202,6 +238,30 @@ void paged_attention_cuda(const float* q, const uint16_t* kv_cache, const int32_
 void flash_attention_cuda(const float* q, const float* k, const float* v, float* out,
                           float* attn_weights, int32_t batch_size, int32_t num_heads,
                           int32_t head_dim, int32_t q_len, int32_t kv_len, const float* attn_mask);
+
+/*
+ * cuda/attention.h:47-56 (apply_rope_cuda), with the reference kernel's
+ * semantics (cuda/attention_kernels.cuh:249-287, launched by
+ * cuda/attention.cu:130-145):
+ *   q, k      [batch_size][total_dim] fp32 on the device, rotated in place
+ *   cos, sin  [head_dim / 2] fp32 on the device, one row for every batch row
+ * Element d (head d / head_dim, hdim = d % head_dim < head_dim / 2) pairs with
+ * d + head_dim / 2, or with itself when that index reaches total_dim (then the
+ * second write, x s + x c, is what remains).  Null stream; returns after the
+ * kernel finished, as the reference does (cudaDeviceSynchronize).
+ */
+void apply_rope_cuda(float* q, float* k, const float* cos, const float* sin, int32_t total_dim,
+                     int32_t head_dim, int32_t batch_size);
+
+/*
+ * cuda/attention.h:58-66 (head_norm_cuda).  The reference launcher defines its
+ * kernel but launches nothing (cuda/attention.cu:152-189); this one does what
+ * its comment states: x [batch_size][num_heads][head_dim] fp32 on the device,
+ * each head scaled in place by weight[d] / sqrt(sum(x^2) / head_dim + eps)
+ * (src/paged_engine.cpp:14-20 per head).  Null stream, returns when done.
+ */
+void head_norm_cuda(float* x, const float* weight, float eps, int32_t num_heads, int32_t head_dim,
+                    int32_t batch_size);
 
 /* ---- instrumentation (no reference counterpart) --------------------------- */
 

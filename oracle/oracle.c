@@ -431,3 +431,65 @@ void orc_flash_attention(const float* q, const float* k, const float* v, float* 
         }
     }
 }
+
+/* ---- query / key preparation ------------------------------------------ */
+
+/* src/paged_engine.cpp:14-20 (rms_norm) applied to each head_dim row: the sum
+ * of squares in order, inv = 1 / sqrt(sum / dim + eps), y = (w * x) * inv. */
+void orc_head_norm(float* x, const float* w, float eps, int64_t rows, int32_t head_dim) {
+    for (int64_t r = 0; r < rows; ++r) {
+        float* xr = x + r * head_dim;
+        float ss = 0.0f;
+        for (int32_t i = 0; i < head_dim; ++i) ss += xr[i] * xr[i];
+        const float inv = 1.0f / sqrtf(ss / (float)head_dim + eps);
+        for (int32_t i = 0; i < head_dim; ++i) xr[i] = w[i] * xr[i] * inv;
+    }
+}
+
+/* src/paged_engine.cpp:47-62 (rope_single) for every token at its own
+ * position: pair i uses inv_freq[min(i, n_freq - 1)] * (float)pos, cosf/sinf,
+ * and the pair (2i, 2i + 1) (style 0) or (i, i + head_dim / 2) (style 1, the
+ * pairing of cuda/attention_kernels.cuh:249-287). */
+void orc_rope(float* x, int32_t num_tokens, int32_t num_heads, int32_t head_dim,
+              const int32_t* positions, const float* inv_freq, int32_t n_freq, int32_t style) {
+    const int32_t half = head_dim / 2;
+    for (int32_t t = 0; t < num_tokens; ++t) {
+        const float pos = (float)positions[t];
+        for (int32_t h = 0; h < num_heads; ++h) {
+            float* xh = x + ((int64_t)t * num_heads + h) * head_dim;
+            for (int32_t i = 0; i < half; ++i) {
+                const int32_t fi = i < n_freq - 1 ? i : n_freq - 1;
+                const float freq = inv_freq[fi] * pos;
+                const float c = cosf(freq), s = sinf(freq);
+                const int32_t i0 = style ? i : 2 * i, i1 = style ? i + half : 2 * i + 1;
+                const float x0 = xh[i0], x1 = xh[i1];
+                xh[i0] = x0 * c - x1 * s;
+                xh[i1] = x0 * s + x1 * c;
+            }
+        }
+    }
+}
+
+/* cuda/attention_kernels.cuh:249-287 as launched by apply_rope_cuda
+ * (cuda/attention.cu:130-145): cos/sin [head_dim / 2] shared by every batch
+ * row; element d with d % head_dim < head_dim / 2 pairs with d + head_dim / 2,
+ * or with itself past total_dim (the second store then wins). */
+void orc_rope_table(float* q, float* k, const float* cs, const float* sn, int32_t total_dim,
+                    int32_t head_dim, int32_t batch) {
+    for (int32_t b = 0; b < batch; ++b) {
+        float* qb = q + (int64_t)b * total_dim;
+        float* kb = k + (int64_t)b * total_dim;
+        for (int32_t d = 0; d < total_dim; ++d) {
+            const int32_t hd = d % head_dim;
+            if (hd >= head_dim / 2) continue;
+            const float c = cs[hd], s = sn[hd];
+            int32_t i1 = d + head_dim / 2;
+            if (i1 >= total_dim) i1 = d;
+            const float q0 = qb[d], q1 = qb[i1], k0 = kb[d], k1 = kb[i1];
+            qb[d] = q0 * c - q1 * s;
+            qb[i1] = q0 * s + q1 * c;
+            kb[d] = k0 * c - k1 * s;
+            kb[i1] = k0 * s + k1 * c;
+        }
+    }
+}

@@ -108,6 +108,16 @@ void orc_fill_uniform_int(uint64_t seed, int32_t* out, int64_t n, int32_t lo, in
 /* Fisher-Yates permutation of 0..n-1 driven by splitmix64. */
 void orc_permutation(uint64_t seed, int32_t* out, int32_t n);
 
+/* Per-head RMS norm, src/paged_engine.cpp:14-20 per row of head_dim (in place). */
+void orc_head_norm(float* x, const float* w, float eps, int64_t rows, int32_t head_dim);
+/* RoPE at per-token positions, src/paged_engine.cpp:47-62; style 0 pairs
+ * (2i, 2i+1), style 1 pairs (i, i + head_dim/2) (in place). */
+void orc_rope(float* x, int32_t num_tokens, int32_t num_heads, int32_t head_dim,
+              const int32_t* positions, const float* inv_freq, int32_t n_freq, int32_t style);
+/* apply_rope_cuda semantics, cuda/attention_kernels.cuh:249-287 (in place). */
+void orc_rope_table(float* q, float* k, const float* cs, const float* sn, int32_t total_dim,
+                    int32_t head_dim, int32_t batch);
+
 #ifdef __cplusplus
 }
 #endif

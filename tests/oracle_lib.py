@@ -11,6 +11,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libref.so")
+REF_ENGINE_SO = os.path.join(ROOT, "oracle", "_ref", "libref_engine.so")
 
 ORC_F32, ORC_F16, ORC_I8 = 0, 1, 2
 BS = 16  # reference BLOCK_SIZE (src/config.h:48)
@@ -69,6 +70,9 @@ def orc():
         L.orc_fill_normal.argtypes = [ctypes.c_uint64, vp, i64, ctypes.c_double, ctypes.c_double]
         L.orc_fill_uniform_int.argtypes = [ctypes.c_uint64, vp, i64, i32, i32]
         L.orc_permutation.argtypes = [ctypes.c_uint64, vp, i32]
+        L.orc_head_norm.argtypes = [vp, vp, ctypes.c_float, i64, i32]
+        L.orc_rope.argtypes = [vp, i32, i32, i32, vp, vp, i32, i32]
+        L.orc_rope_table.argtypes = [vp, vp, vp, vp, i32, i32, i32]
         _orc = L
     return _orc
 
@@ -286,3 +290,63 @@ def flash(q, k, v, mask=None):
     orc().orc_flash_attention(_p(q), _p(k), _p(v), _p(out), _p(w), B, H, D, ql, kv,
                               None if m is None else _p(m))
     return out, w
+
+
+# ---- query / key preparation ------------------------------------------------
+
+ROPE_INTERLEAVED, ROPE_HALF = 0, 1
+
+
+def head_norm(x, w, eps):
+    """orc_head_norm on x [..., head_dim] (returns a new array)."""
+    y = np.array(x, np.float32, copy=True, order="C")
+    w = np.ascontiguousarray(w, np.float32)
+    D = y.shape[-1]
+    orc().orc_head_norm(_p(y), _p(w), ctypes.c_float(eps), y.size // D, D)
+    return y
+
+
+def rope(x, positions, inv_freq, style):
+    """orc_rope on x [tokens][heads][head_dim] (returns a new array)."""
+    y = np.array(x, np.float32, copy=True, order="C")
+    T, H, D = y.shape
+    pos = np.ascontiguousarray(positions, np.int32)
+    f = np.ascontiguousarray(inv_freq, np.float32)
+    orc().orc_rope(_p(y), T, H, D, _p(pos), _p(f), len(f), style)
+    return y
+
+
+def rope_table(q, k, cs, sn, head_dim):
+    """orc_rope_table on q, k [batch][total_dim] (returns new arrays)."""
+    q = np.array(q, np.float32, copy=True, order="C")
+    k = np.array(k, np.float32, copy=True, order="C")
+    cs = np.ascontiguousarray(cs, np.float32)
+    sn = np.ascontiguousarray(sn, np.float32)
+    B, total = q.shape
+    orc().orc_rope_table(_p(q), _p(k), _p(cs), _p(sn), total, head_dim, B)
+    return q, k
+
+
+def inv_freq_table(head_dim, base=1000000.0):
+    """The engine's default table: 1 / base^(2i / head_dim) in fp32
+    (src/model.cpp:582-588, ROPE_BASE src/config.h:43)."""
+    i = np.arange(head_dim // 2, dtype=np.float32)
+    return (1.0 / np.power(np.float32(base), (np.float32(2.0) * i) / np.float32(head_dim))).astype(np.float32)
+
+
+_ref_engine = None
+
+
+def ref_engine_available():
+    return os.path.exists(REF_ENGINE_SO)
+
+
+def ref_engine():
+    global _ref_engine
+    if _ref_engine is None:
+        L = ctypes.CDLL(REF_ENGINE_SO)
+        vp, i32 = ctypes.c_void_p, ctypes.c_int32
+        L.ref_rope_single.argtypes = [vp, i32, i32, i32, vp, i32]
+        L.ref_rms_norm.argtypes = [vp, vp, vp, i32, ctypes.c_float]
+        _ref_engine = L
+    return _ref_engine

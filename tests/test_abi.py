@@ -99,3 +99,36 @@ def test_flash_rejects_empty_kv():
     assert "kv_len 0" in pyvcpp.last_error()
     L.flash_attention_cuda(None, dummy, dummy, dummy, dummy, 1, 1, 80, 1, 4, None)
     assert "NULL" in pyvcpp.last_error()
+
+
+def test_qk_prep_argument_errors():
+    """Shape, style and table checks of vcpp_qk_norm_rope / vcpp_rope /
+    vcpp_head_norm run before any HIP call."""
+    L = pyvcpp.lib()
+    p = ctypes.c_void_p(4096)
+    f = ctypes.c_float
+    assert L.vcpp_qk_norm_rope(p, None, 4, 8, 0, 81, None, None, f(0), p, p, 40, 0, None) == \
+        pyvcpp.VCPP_E_UNSUPPORTED
+    assert "head_dim 81" in pyvcpp.last_error()
+    assert L.vcpp_qk_norm_rope(p, None, 4, 8, 0, 512, None, None, f(0), p, p, 40, 0, None) == \
+        pyvcpp.VCPP_E_UNSUPPORTED
+    assert L.vcpp_qk_norm_rope(p, None, 4, 8, 0, 80, None, None, f(0), p, p, 40, 7, None) == \
+        pyvcpp.VCPP_E_INVALID
+    assert "style" in pyvcpp.last_error()
+    assert L.vcpp_qk_norm_rope(p, None, 4, 8, 0, 80, None, None, f(0), p, None, 0, 0, None) == \
+        pyvcpp.VCPP_E_INVALID
+    assert "inv_freq" in pyvcpp.last_error()
+    assert L.vcpp_qk_norm_rope(p, p, 4, 8, 0, 80, None, None, f(0), p, p, 40, 0, None) == \
+        pyvcpp.VCPP_E_INVALID
+    assert L.vcpp_qk_norm_rope(p, None, 4, 8, 0, 80, p, None, f(-1.0), None, None, 0, 0, None) == \
+        pyvcpp.VCPP_E_INVALID
+    assert "eps" in pyvcpp.last_error()
+    assert L.vcpp_rope(p, 4, 8, 80, None, p, 40, 0, None) == pyvcpp.VCPP_E_INVALID
+    assert L.vcpp_head_norm(p, None, f(1e-6), 4, 80, None) == pyvcpp.VCPP_E_INVALID
+    # nothing to do: no launch, OK
+    assert L.vcpp_qk_norm_rope(None, None, 0, 8, 0, 80, None, None, f(0), None, None, 0, 0, None) == \
+        pyvcpp.VCPP_OK
+    L.apply_rope_cuda(None, p, p, p, 160, 80, 2)
+    assert "NULL" in pyvcpp.last_error()
+    L.apply_rope_cuda(p, p, p, p, 160, 1, 2)
+    assert "head_dim 1" in pyvcpp.last_error()

@@ -19,6 +19,7 @@
 #include "prefill.h"
 #include "dense.h"
 #include "kv_write.h"
+#include "qk_prep.h"
 #include "vcpp_attention.h"
 
 namespace {
@@ -34,6 +35,8 @@ int fail(int code, const char* fmt, ...) {
     g_last_error = buf;
     return code;
 }
+
+bool eps_ok(float eps) { return std::isfinite(eps) && eps >= 0.f; }
 
 int hip_fail(hipError_t e, const char* what) {
     return fail(VCPP_E_HIP, "%s: %s", what, hipGetErrorString(e));
@@ -167,6 +170,65 @@ int check_pages(const vcpp_kv_pages* kv) {
 }
 
 }  // namespace
+
+// ---- v2: query / key preparation ------------------------------------------
+
+int vcpp_qk_norm_rope(float* q, float* k, int32_t num_tokens, int32_t num_heads,
+                      int32_t num_kv_heads, int32_t head_dim, const float* q_norm_weight,
+                      const float* k_norm_weight, float eps, const int32_t* positions,
+                      const float* inv_freq, int32_t inv_freq_size, int32_t style, void* stream) {
+    g_last_error.clear();
+    if (num_tokens < 0 || num_heads <= 0 || (k && num_kv_heads <= 0))
+        return fail(VCPP_E_INVALID, "num_tokens %d, num_heads %d, num_kv_heads %d", num_tokens,
+                    num_heads, num_kv_heads);
+    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > 256)
+        return fail(VCPP_E_UNSUPPORTED, "head_dim %d must be even and <= 256", head_dim);
+    if (style != VCPP_ROPE_INTERLEAVED && style != VCPP_ROPE_HALF)
+        return fail(VCPP_E_INVALID, "unknown rope style %d", style);
+    if (positions && (!inv_freq || inv_freq_size <= 0))
+        return fail(VCPP_E_INVALID, "rotation needs inv_freq with inv_freq_size > 0");
+    if (!eps_ok(eps)) return fail(VCPP_E_INVALID, "eps must be finite and >= 0");
+    if (num_tokens == 0) return VCPP_OK;
+    if (!q) return fail(VCPP_E_INVALID, "q is NULL");
+    if (reinterpret_cast<uintptr_t>(q) % 8 != 0 || reinterpret_cast<uintptr_t>(k) % 8 != 0)
+        return fail(VCPP_E_INVALID, "q and k must be 8-byte aligned");
+    const int64_t rows = (int64_t)num_tokens * num_heads + (k ? (int64_t)num_tokens * num_kv_heads : 0);
+    if (rows > (int64_t)INT32_MAX * 4) return fail(VCPP_E_UNSUPPORTED, "too many rows");
+    vcpp::QkPrepParams p{};
+    p.t[0] = {q, q_norm_weight, num_heads};
+    p.t[1] = {k, k_norm_weight, k ? num_kv_heads : 0};
+    p.num_tokens = num_tokens;
+    p.head_dim = head_dim;
+    p.eps = eps;
+    p.positions = positions;
+    p.inv_freq = inv_freq;
+    p.inv_freq_size = inv_freq_size;
+    p.style = style;
+    const hipError_t e = vcpp::launch_qk_prep(p, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "qk_prep launch");
+    return VCPP_OK;
+}
+
+int vcpp_rope(float* x, int32_t num_tokens, int32_t num_heads, int32_t head_dim,
+              const int32_t* positions, const float* inv_freq, int32_t inv_freq_size,
+              int32_t style, void* stream) {
+    if (!positions && num_tokens > 0) {
+        g_last_error.clear();
+        return fail(VCPP_E_INVALID, "positions is NULL");
+    }
+    return vcpp_qk_norm_rope(x, nullptr, num_tokens, num_heads, 0, head_dim, nullptr, nullptr, 0.f,
+                             positions, inv_freq, inv_freq_size, style, stream);
+}
+
+int vcpp_head_norm(float* x, const float* weight, float eps, int32_t num_rows, int32_t head_dim,
+                   void* stream) {
+    if (!weight && num_rows > 0) {
+        g_last_error.clear();
+        return fail(VCPP_E_INVALID, "weight is NULL");
+    }
+    return vcpp_qk_norm_rope(x, nullptr, num_rows, 1, 0, head_dim, weight, nullptr, eps, nullptr,
+                             nullptr, 0, VCPP_ROPE_INTERLEAVED, stream);
+}
 
 // ---- v1 shims: library-owned buffers ---------------------------------------
 
@@ -457,6 +519,44 @@ void flash_attention_cuda(const float* q, const float* k, const float* v, float*
     vcpp::DenseParams p{q, k, v, out, attn_weights, attn_mask, batch_size, num_heads, head_dim, q_len, kv_len};
     const hipError_t e = vcpp::launch_dense(p, nullptr);
     if (e != hipSuccess) hip_fail(e, "flash_attention_cuda launch");
+}
+
+void apply_rope_cuda(float* q, float* k, const float* cos, const float* sin, int32_t total_dim,
+                     int32_t head_dim, int32_t batch_size) {
+    g_last_error.clear();
+    if (batch_size <= 0 || total_dim <= 0) return;
+    if (!q || !k || !cos || !sin) {
+        fail(VCPP_E_INVALID, "apply_rope_cuda: q/k/cos/sin is NULL");
+        return;
+    }
+    if (head_dim < 2) {
+        fail(VCPP_E_INVALID, "apply_rope_cuda: head_dim %d must be >= 2", head_dim);
+        return;
+    }
+    if ((int64_t)batch_size * total_dim > (int64_t)INT32_MAX * 256) {
+        fail(VCPP_E_UNSUPPORTED, "apply_rope_cuda: shape too large");
+        return;
+    }
+    vcpp::RopeTableParams p{q, k, cos, sin, total_dim, head_dim, batch_size};
+    hipError_t e = vcpp::launch_rope_table(p, nullptr);
+    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) hip_fail(e, "apply_rope_cuda");
+}
+
+void head_norm_cuda(float* x, const float* weight, float eps, int32_t num_heads, int32_t head_dim,
+                    int32_t batch_size) {
+    if (batch_size <= 0 || num_heads <= 0) {
+        g_last_error.clear();
+        return;
+    }
+    if ((int64_t)batch_size * num_heads > INT32_MAX) {
+        g_last_error.clear();
+        fail(VCPP_E_UNSUPPORTED, "head_norm_cuda: shape too large");
+        return;
+    }
+    if (vcpp_head_norm(x, weight, eps, batch_size * num_heads, head_dim, nullptr) != VCPP_OK) return;
+    const hipError_t e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) hip_fail(e, "head_norm_cuda");
 }
 
 }  // extern "C"

@@ -30,6 +30,11 @@ EXPORTS = [
     "vcpp_decode_workspace_size",
     "vcpp_paged_prefill",
     "vcpp_write_kv",
+    "vcpp_qk_norm_rope",
+    "vcpp_rope",
+    "vcpp_head_norm",
+    "apply_rope_cuda",
+    "head_norm_cuda",
     "paged_attention_cuda",
     "flash_attention_cuda",
     "vcpp_profile_enable",
@@ -86,6 +91,17 @@ def lib():
     L.vcpp_paged_prefill.restype = ctypes.c_int
     L.vcpp_write_kv.argtypes = [ctypes.POINTER(KVPages), vp, vp, vp, i32, i32, vp]
     L.vcpp_write_kv.restype = ctypes.c_int
+    L.vcpp_qk_norm_rope.argtypes = [vp, vp, i32, i32, i32, i32, vp, vp, ctypes.c_float, vp, vp,
+                                    i32, i32, vp]
+    L.vcpp_qk_norm_rope.restype = ctypes.c_int
+    L.vcpp_rope.argtypes = [vp, i32, i32, i32, vp, vp, i32, i32, vp]
+    L.vcpp_rope.restype = ctypes.c_int
+    L.vcpp_head_norm.argtypes = [vp, vp, ctypes.c_float, i32, i32, vp]
+    L.vcpp_head_norm.restype = ctypes.c_int
+    L.apply_rope_cuda.argtypes = [vp, vp, vp, vp, i32, i32, i32]
+    L.apply_rope_cuda.restype = None
+    L.head_norm_cuda.argtypes = [vp, vp, ctypes.c_float, i32, i32, i32]
+    L.head_norm_cuda.restype = None
     L.paged_attention_cuda.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32]
     L.paged_attention_cuda.restype = None
     L.flash_attention_cuda.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]
@@ -180,3 +196,50 @@ def write_kv(pages, k, v, slots, fp16_round_nearest=False, stream=None):
     rc = lib().vcpp_write_kv(ctypes.byref(pages), _ptr(k), _ptr(v), _ptr(slots), k.shape[0],
                              1 if fp16_round_nearest else 0, _stream(stream))
     _check(rc)
+
+
+ROPE_INTERLEAVED, ROPE_HALF = 0, 1
+
+
+def qk_norm_rope(q, k=None, positions=None, inv_freq=None, q_norm_weight=None, k_norm_weight=None,
+                 eps=1e-6, style=ROPE_INTERLEAVED, stream=None):
+    """vcpp_qk_norm_rope in place on q [T][H][D] and k [T][Hkv][D] (fp32 device tensors)."""
+    T, H, D = q.shape
+    Hkv = k.shape[1] if k is not None else 0
+    nf = inv_freq.numel() if inv_freq is not None else 0
+    rc = lib().vcpp_qk_norm_rope(_ptr(q), _ptr(k), T, H, Hkv, D, _ptr(q_norm_weight),
+                                 _ptr(k_norm_weight), ctypes.c_float(eps), _ptr(positions),
+                                 _ptr(inv_freq), nf, style, _stream(stream))
+    _check(rc)
+
+
+def rope(x, positions, inv_freq, style=ROPE_INTERLEAVED, stream=None):
+    """vcpp_rope in place on x [T][H][D]."""
+    T, H, D = x.shape
+    _check(lib().vcpp_rope(_ptr(x), T, H, D, _ptr(positions), _ptr(inv_freq), inv_freq.numel(),
+                           style, _stream(stream)))
+
+
+def head_norm(x, weight, eps, stream=None):
+    """vcpp_head_norm in place on x [..., D]."""
+    D = x.shape[-1]
+    _check(lib().vcpp_head_norm(_ptr(x), _ptr(weight), ctypes.c_float(eps), x.numel() // D, D,
+                                _stream(stream)))
+
+
+def apply_rope_cuda(q, k, cos, sin, head_dim):
+    """v1 apply_rope_cuda on q, k [B][total_dim]; raises on a recorded error."""
+    B, total = q.shape
+    lib().apply_rope_cuda(_ptr(q), _ptr(k), _ptr(cos), _ptr(sin), total, head_dim, B)
+    err = last_error()
+    if err:
+        raise VcppError(VCPP_E_INVALID, err)
+
+
+def head_norm_cuda(x, weight, eps):
+    """v1 head_norm_cuda on x [B][H][D]; raises on a recorded error."""
+    B, H, D = x.shape
+    lib().head_norm_cuda(_ptr(x), _ptr(weight), ctypes.c_float(eps), H, D, B)
+    err = last_error()
+    if err:
+        raise VcppError(VCPP_E_INVALID, err)
