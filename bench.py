@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the config 4 (long context) and config 5 (int8 mixed) legs")
     ap.add_argument("--config-steps", type=int, default=20)
-    ap.add_argument("--only", choices=["decode", "prefill", "config4", "config5"],
+    ap.add_argument("--only", choices=["decode", "prefill", "config4", "config5", "qkprep"],
                     help="run one leg only and print its JSON (for profiling)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the prefill leg (for profiling its kernel)")
@@ -356,6 +356,46 @@ def read_traffic(name):
     return None
 
 
+def bench_qkprep(torch, pyvcpp, args):
+    """Fused q/k norm + RoPE (vcpp_qk_norm_rope) over config 3's 16384 prefill
+    tokens: q [16384][64][80], k [16384][8][80] fp32 at positions 1024..3071,
+    per-head RMS norm then interleaved rotation, in place.  HBM-bound: every
+    element read once and written once (plus positions and the norm weights)."""
+    dev = torch.device("cuda:0")
+    T = 8 * 2048
+    g = torch.Generator(device=dev).manual_seed(args.seed + 60)
+    q = torch.randn((T, H, D), generator=g, device=dev)
+    k = torch.randn((T, HKV, D), generator=g, device=dev)
+    pos = (torch.arange(T, dtype=torch.int32, device=dev) % 2048) + 1024
+    i = torch.arange(D // 2, dtype=torch.float32, device=dev)
+    inv_freq = 1.0 / torch.pow(torch.tensor(1e6, device=dev), 2.0 * i / D)
+    qw = torch.ones(D, device=dev) + 0.1 * torch.randn(D, generator=g, device=dev)
+    kw = torch.ones(D, device=dev) + 0.1 * torch.randn(D, generator=g, device=dev)
+    nbytes = 2 * (q.numel() + k.numel()) * 4 + T * 4 + 2 * D * 4 + (D // 2) * 4
+
+    def step():
+        pyvcpp.qk_norm_rope(q, k, pos, inv_freq, qw, kw, 1e-6, pyvcpp.ROPE_INTERLEAVED)
+    steps = max(args.config_steps, 10)
+    dt = timed(torch, step, steps)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    k_s = e0.elapsed_time(e1) / steps / 1e3
+    return {
+        "metric": "q/k norm + RoPE HBM TB/s", "value": round(nbytes / dt / 1e12, 3), "unit": "TB/s",
+        "ms_per_step": round(dt * 1e3, 4), "steps": steps,
+        "config": {"workload": "config 3 tokens: 16384 x (64 q + 8 k heads) x 80 fp32, q_norm/k_norm "
+                               "then interleaved RoPE at positions 1024..3071, in place",
+                   "bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(nbytes / k_s / 1e9, 1), "peak": HBM_PEAK_TBS * 1e3,
+                     "unit": "GB/s", "frac": round(nbytes / k_s / 1e12 / HBM_PEAK_TBS, 4),
+                     "kernel": "qk_prep_kernel", "kernel_avg_us": round(k_s * 1e6, 2)},
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -385,6 +425,9 @@ def main():
         return
     if args.only == "config5":
         print(json.dumps(bench_config5(torch, pyvcpp, args)))
+        return
+    if args.only == "qkprep":
+        print(json.dumps(bench_qkprep(torch, pyvcpp, args)))
         return
 
     w = decode_workload(torch, args.seed)
@@ -445,6 +488,7 @@ def main():
     if not args.no_configs:
         result["config4"] = bench_config4(torch, pyvcpp, args)
         result["config5"] = bench_config5(torch, pyvcpp, args)
+        result["qk_prep"] = bench_qkprep(torch, pyvcpp, args)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(torch, w, args.cpu_seconds)
     else:

@@ -226,8 +226,11 @@ int vcpp_head_norm(float* x, const float* weight, float eps, int32_t num_rows, i
         g_last_error.clear();
         return fail(VCPP_E_INVALID, "weight is NULL");
     }
-    return vcpp_qk_norm_rope(x, nullptr, num_rows, 1, 0, head_dim, weight, nullptr, eps, nullptr,
-                             nullptr, 0, VCPP_ROPE_INTERLEAVED, stream);
+    // Rows go to the kernel's waves in runs of up to 16 (one "token" each).
+    int run = 16;
+    while (run > 1 && num_rows % run != 0) run /= 2;
+    return vcpp_qk_norm_rope(x, nullptr, num_rows / run, run, 0, head_dim, weight, nullptr, eps,
+                             nullptr, nullptr, 0, VCPP_ROPE_INTERLEAVED, stream);
 }
 
 // ---- v1 shims: library-owned buffers ---------------------------------------
@@ -554,7 +557,14 @@ void head_norm_cuda(float* x, const float* weight, float eps, int32_t num_heads,
         fail(VCPP_E_UNSUPPORTED, "head_norm_cuda: shape too large");
         return;
     }
-    if (vcpp_head_norm(x, weight, eps, batch_size * num_heads, head_dim, nullptr) != VCPP_OK) return;
+    if (!weight) {
+        g_last_error.clear();
+        fail(VCPP_E_INVALID, "head_norm_cuda: weight is NULL");
+        return;
+    }
+    if (vcpp_qk_norm_rope(x, nullptr, batch_size, num_heads, 0, head_dim, weight, nullptr, eps,
+                          nullptr, nullptr, 0, VCPP_ROPE_INTERLEAVED, nullptr) != VCPP_OK)
+        return;
     const hipError_t e = hipStreamSynchronize(nullptr);
     if (e != hipSuccess) hip_fail(e, "head_norm_cuda");
 }

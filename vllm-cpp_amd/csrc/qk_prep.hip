@@ -1,10 +1,11 @@
 // qk_prep.hip -- query/key preparation in front of attention: the per-head RMS
 // norm of Qwen3-style models and the rotary position embedding (RoPE).
 //
-// qk_prep_kernel: one wave per (token, head) row of q or k, lane i owning the
-// rotation pair i (pairs per row <= 64 per pass, head_dim <= 256).  Each row is
-// read once and written once: norm (optional) then rotation (optional), the
-// order of Qwen3 (q_norm / k_norm before the rotary embedding).  Arithmetic
+// qk_prep_kernel: one wave per (token, 16 head rows of q or k), lane L owning
+// elements L, L + 64, ... of each row.  Each
+// row is read once and written once: norm (optional) then rotation
+// (optional), the order of Qwen3 (q_norm / k_norm before the rotary
+// embedding).  Arithmetic
 // follows the reference statement by statement with contraction off:
 //   norm  inv = 1 / sqrt(sum(x^2) / head_dim + eps); y = (w * x) * inv
 //         (src/paged_engine.cpp:14-20, applied per head);
@@ -12,8 +13,10 @@
 //         s = sin(theta); (x0, x1) -> (x0 c - x1 s, x0 s + x1 c), with the pair
 //         (2i, 2i + 1) (src/paged_engine.cpp:47-62) or (i, i + head_dim / 2)
 //         (cuda/attention_kernels.cuh:249-287).
-// The row reduction is a lane tree, so the norm matches the reference's
-// sequential sum to fp32 rounding, not bit for bit.
+// The row reduction is a lane tree and 1 / sqrt uses the hardware square root
+// and reciprocal, so the norm matches the reference to a few fp32 ulps, not
+// bit for bit; the rotation partner is
+// the partner's normalised value, as in the reference's sequence of calls.
 //
 // rope_table_kernel: apply_rope_cuda (cuda/attention.cu:130-145) -- one thread
 // per (batch row, d) with d in the first half of its head, cos/sin indexed by
@@ -27,79 +30,116 @@ namespace vcpp {
 namespace {
 
 constexpr int kQkWaves = 4;
+constexpr int kRows = 16;  // head rows per wave
 
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                 0xF, 0xF, false));
+}
+
+// Sum over the wave's 64 lanes, bitwise identical in every lane (each step
+// adds two equal-shape partial sums, and fp32 addition commutes): quad swaps,
+// half-row and row mirrors (DPP), then the two cross-row steps.
+__device__ __forceinline__ float wave_allsum(float v) {
+    v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp<0x141>(v);  // row_half_mirror
+    v += dpp<0x140>(v);  // row_mirror
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+// One wave per (token, group of kRows head rows of q or of k); the group
+// shares the token's cos/sin.  Lane L owns
+// element e = L + 64 j of each row (NE = ceil(head_dim / 64) per lane), so a
+// row moves in fully coalesced 256-byte instructions.  The rotation partner of
+// e is e ^ 1 (interleaved: the neighbouring lane, by a DPP quad swap) or
+// e +- head_dim / 2 (half-split: loaded again, from cache).
+template <int NE>
 __global__ __launch_bounds__(kQkWaves * 64) void qk_prep_kernel(QkPrepParams p) {
     const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * kQkWaves + (threadIdx.x >> 6);
-    const int64_t rows_q = (int64_t)p.num_tokens * p.t[0].num_heads;
-    const int64_t rows_k = p.t[1].x ? (int64_t)p.num_tokens * p.t[1].num_heads : 0;
-    if (row >= rows_q + rows_k) return;
-    const int which = row >= rows_q;
-    const QkTensor& T = p.t[which];
-    const int64_t r = which ? row - rows_q : row;
-    const int64_t tok = r / T.num_heads;
-    float* x = T.x + r * p.head_dim;
+    // wave-uniform work item (scalar registers, scalar branches)
+    const int64_t item = (int64_t)blockIdx.x * kQkWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int gq = (p.t[0].num_heads + kRows - 1) / kRows;
+    const int gk = p.t[1].x ? (p.t[1].num_heads + kRows - 1) / kRows : 0;
+    const int64_t tok = item / (gq + gk);
+    if (tok >= p.num_tokens) return;
+    const int grp = (int)(item - tok * (gq + gk));
+    const int which = grp >= gq;
+    const QkTensor T = p.t[which];
+    const int h0 = (which ? grp - gq : grp) * kRows;
+    const int nrows = min(kRows, T.num_heads - h0);
     const int D = p.head_dim, P = D / 2;
     const bool half = p.style == VCPP_ROPE_HALF;
-    constexpr int kMaxPairs = 2;  // head_dim <= 256
-    float x0[kMaxPairs], x1[kMaxPairs];
+    const bool rot = p.positions != nullptr;
+    const bool norm = T.norm_weight != nullptr;
+    float* base = T.x + (tok * T.num_heads + h0) * D;
+
+    // Element e = lane + 64 j of each row; lanes past the row read a valid
+    // element (discarded) instead of branching.
+    int ei[NE], pe[NE];
+    bool first[NE], valid[NE];
 #pragma unroll
-    for (int j = 0; j < kMaxPairs; ++j) {
-        const int i = lane + 64 * j;
-        x0[j] = x1[j] = 0.f;
-        if (i < P) {
-            if (half) {
-                x0[j] = x[i];
-                x1[j] = x[i + P];
-            } else {
-                const float2 v = *reinterpret_cast<const float2*>(x + 2 * i);
-                x0[j] = v.x;
-                x1[j] = v.y;
-            }
+    for (int j = 0; j < NE; ++j) {
+        const int e = lane + 64 * j;
+        valid[j] = e < D;
+        const int ec = valid[j] ? e : lane % D;
+        ei[j] = ec;
+        first[j] = half ? ec < P : (ec & 1) == 0;
+        pe[j] = half ? (ec < P ? ec + P : ec - P) : (ec ^ 1);
+    }
+    float x[kRows][NE], xp[kRows][NE];
+    // rows past nrows re-read the last row (cache hits) instead of branching
+#pragma unroll
+    for (int u = 0; u < kRows; ++u) {
+        const int ur = min(u, nrows - 1);
+#pragma unroll
+        for (int j = 0; j < NE; ++j) {
+            x[u][j] = base[ur * D + ei[j]];
+            xp[u][j] = (half && rot) ? base[ur * D + pe[j]] : 0.f;
         }
     }
-    if (T.norm_weight) {
-        float ss = 0.f;
+    float cs[NE], sn[NE], w[NE], wp[NE];
+    const float pos = rot ? (float)p.positions[tok] : 0.f;
 #pragma unroll
-        for (int j = 0; j < kMaxPairs; ++j) ss += x0[j] * x0[j] + x1[j] * x1[j];
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
-        const float inv = 1.0f / sqrtf(ss / (float)D + p.eps);
-#pragma unroll
-        for (int j = 0; j < kMaxPairs; ++j) {
-            const int i = lane + 64 * j;
-            if (i < P) {
-                const int d0 = half ? i : 2 * i, d1 = half ? i + P : 2 * i + 1;
-                x0[j] = T.norm_weight[d0] * x0[j] * inv;
-                x1[j] = T.norm_weight[d1] * x1[j] * inv;
-            }
+    for (int j = 0; j < NE; ++j) {
+        cs[j] = 1.f;
+        sn[j] = 0.f;
+        w[j] = wp[j] = 1.f;
+        if (rot) {
+            const int pi = half ? (ei[j] < P ? ei[j] : ei[j] - P) : (ei[j] >> 1);
+            sincosf(p.inv_freq[min(pi, p.inv_freq_size - 1)] * pos, &sn[j], &cs[j]);
+        }
+        if (norm) {
+            w[j] = T.norm_weight[ei[j]];
+            wp[j] = T.norm_weight[pe[j]];
         }
     }
-    if (p.positions) {
-        const float pos = (float)p.positions[tok];
+    const float inv_d = 1.0f / (float)D;
 #pragma unroll
-        for (int j = 0; j < kMaxPairs; ++j) {
-            const int i = lane + 64 * j;
-            if (i < P) {
-                const float theta = p.inv_freq[min(i, p.inv_freq_size - 1)] * pos;
-                float s, c;
-                sincosf(theta, &s, &c);
-                const float a = x0[j], b = x1[j];
-                x0[j] = a * c - b * s;
-                x1[j] = a * s + b * c;
-            }
+    for (int u = 0; u < kRows; ++u) {
+        float inv = 1.f;
+        if (norm) {
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < NE; ++j) ss += valid[j] ? x[u][j] * x[u][j] : 0.f;
+            ss = wave_allsum(ss);
+            // hardware sqrt and reciprocal (about 1 ulp each)
+            inv = __builtin_amdgcn_rcpf(__builtin_amdgcn_sqrtf(ss * inv_d + p.eps));
         }
-    }
 #pragma unroll
-    for (int j = 0; j < kMaxPairs; ++j) {
-        const int i = lane + 64 * j;
-        if (i < P) {
-            if (half) {
-                x[i] = x0[j];
-                x[i + P] = x1[j];
-            } else {
-                *reinterpret_cast<float2*>(x + 2 * i) = make_float2(x0[j], x1[j]);
+        for (int j = 0; j < NE; ++j) {
+            float y = norm ? w[j] * x[u][j] * inv : x[u][j];
+            if (rot) {
+                float yp;
+                if (half) yp = norm ? wp[j] * xp[u][j] * inv : xp[u][j];
+                else yp = dpp<0xB1>(y);  // the neighbour's (normalised) value
+                // (x0, x1) -> (x0 c - x1 s, x0 s + x1 c)
+                y = first[j] ? y * cs[j] - yp * sn[j] : yp * sn[j] + y * cs[j];
             }
+            if (u < nrows && valid[j]) base[u * D + ei[j]] = y;
         }
     }
 }
@@ -127,11 +167,14 @@ __global__ __launch_bounds__(256) void rope_table_kernel(RopeTableParams p) {
 }  // namespace
 
 hipError_t launch_qk_prep(const QkPrepParams& p, hipStream_t stream) {
-    const int64_t rows = (int64_t)p.num_tokens * p.t[0].num_heads +
-                         (p.t[1].x ? (int64_t)p.num_tokens * p.t[1].num_heads : 0);
-    if (rows == 0) return hipSuccess;
-    const int64_t wg = (rows + kQkWaves - 1) / kQkWaves;
-    hipLaunchKernelGGL(qk_prep_kernel, dim3((unsigned)wg), dim3(kQkWaves * 64), 0, stream, p);
+    if (p.num_tokens == 0) return hipSuccess;
+    const int64_t groups = (p.t[0].num_heads + kRows - 1) / kRows +
+                           (p.t[1].x ? (p.t[1].num_heads + kRows - 1) / kRows : 0);
+    const int64_t wg = ((int64_t)p.num_tokens * groups + kQkWaves - 1) / kQkWaves;
+    const dim3 grid((unsigned)wg), block(kQkWaves * 64);
+    if (p.head_dim <= 64) hipLaunchKernelGGL(qk_prep_kernel<1>, grid, block, 0, stream, p);
+    else if (p.head_dim <= 128) hipLaunchKernelGGL(qk_prep_kernel<2>, grid, block, 0, stream, p);
+    else hipLaunchKernelGGL(qk_prep_kernel<4>, grid, block, 0, stream, p);
     return hipGetLastError();
 }
 
