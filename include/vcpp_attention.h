@@ -52,6 +52,8 @@ const char* vcpp_version(void);
 #define VCPP_KV_F32 0
 #define VCPP_KV_F16 1
 #define VCPP_KV_I8 2 /* symmetric int8, one fp16 scale per (token, kv head) */
+#define VCPP_KV_FP8 3 /* FP8 E4M3 as the reference KV pool stores it (KVDtype::FP8_E4M3,
+                         src/quantization.cpp:25-82): bias 7, max finite 240, no scales */
 
 /*
  * One layer of a paged KV pool.  Block b's K page is
@@ -63,9 +65,13 @@ const char* vcpp_version(void);
  * block_stride = num_layers * block_size * kv_dim.
  * VCPP_KV_I8 adds fp16 scale pages: block b's K scales are
  *   k_scale + b * scale_block_stride,  laid out [num_kv_heads][block_size].
+ * VCPP_KV_FP8 pages hold one byte per value and no scales.  Codes with
+ * exponent 15 (the reference's +-inf and NaN, which its encoder produces only
+ * from non-finite inputs) are read by the attention kernels as the OCP E4M3
+ * values (0x78-0x7E: 256-448, 0x7F: NaN); every other code decodes exactly.
  * Requirements: head_dim % 16 == 0, block_size % 16 == 0, 16-byte aligned
  * bases and row starts (block_stride * elem_size and head_dim * elem_size
- * multiples of 16 for F16/F32, of 8 for I8).
+ * multiples of 16 for F16/F32, of 8 for I8 and FP8).
  */
 typedef struct vcpp_kv_pages {
     int32_t dtype;
@@ -95,7 +101,7 @@ typedef struct vcpp_kv_pages {
  *                a larger context_len is an error the kernel cannot report:
  *                positions past max_context_len are not attended)
  *   partition_size   0 (default): the tiles of all sequences are split
- *                evenly over the workgroups the GPU holds at once (fp16/int8)
+ *                evenly over the workgroups the GPU holds at once (fp16/int8/fp8)
  *                or into 256-token partitions (fp32).  > 0 (a multiple of 16,
  *                <= 1024): about that many tokens per workgroup range or
  *                partition -- a tuning and test knob.  Ranges that end inside a
@@ -134,7 +140,7 @@ size_t vcpp_decode_workspace_size(const vcpp_kv_pages* kv, int32_t num_seqs, int
  *   q_start      [num_chunks + 1] int32 on the device (q_start[0] == 0)
  *   prefix_lens  [num_chunks] int32 on the device
  *   max_chunk_len host-side upper bound of the chunk lengths (sizes the grid)
- * KV dtypes: VCPP_KV_F16 and VCPP_KV_I8 (int8 is dequantised to fp16 on the
+ * KV dtypes: VCPP_KV_F16, VCPP_KV_I8 and VCPP_KV_FP8 (byte pages are widened to fp16 on the
  * way into LDS); head_dim 64, 80 or 128; num_heads / num_kv_heads any.
  * Replaces read_kv_prefill + compute_attention per position
  * (src/paged_attention.cpp:174-201, src/paged_engine.cpp:64-113,381-384).
@@ -266,7 +272,7 @@ void head_norm_cuda(float* x, const float* weight, float eps, int32_t num_heads,
 /* ---- instrumentation (no reference counterpart) --------------------------- */
 
 /* Kernel ids for vcpp_profile_read. */
-#define VCPP_KERNEL_DECODE 0  /* decode attention (fp16/int8 MFMA or fp32) */
+#define VCPP_KERNEL_DECODE 0  /* decode attention (fp16/int8/fp8 MFMA or fp32) */
 #define VCPP_KERNEL_MERGE 1   /* split-K log-sum-exp merge */
 #define VCPP_KERNEL_PREFILL 2 /* chunked causal prefill */
 

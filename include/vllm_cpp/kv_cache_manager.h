@@ -10,8 +10,9 @@
 //     float (the reference returns a view that is writable for FP32 pools);
 //   * INT8 pools (not in the reference) carry fp16 scale pages
 //     [num_blocks][num_layers][num_kv_heads][BLOCK_SIZE]; they need head_dim;
-//   * FP8_E4M3 is rejected (std::invalid_argument); HIP failures throw
-//     std::runtime_error (the reference has no failure mode there).
+//   * FP8_E4M3 pools hold the reference's E4M3 bytes (VCPP_KV_FP8 pages);
+//     HIP failures throw std::runtime_error (the reference has no failure
+//     mode there).
 // Device work is queued on the pool's stream (default: the null stream).
 #pragma once
 

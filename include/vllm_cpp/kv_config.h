@@ -13,7 +13,7 @@ constexpr int32_t BLOCK_SIZE = 16;
 enum class KVDtype : uint8_t {
     FP32 = 0,
     FP16 = 1,
-    FP8_E4M3 = 2,  // declared for source compatibility; not supported on the GPU
+    FP8_E4M3 = 2,  // the reference's E4M3 (src/quantization.cpp:25-82): VCPP_KV_FP8 pages
     INT8 = 3,      // symmetric int8, one fp16 scale per (token, kv head)
 };
 #endif

@@ -16,6 +16,52 @@
 #include <stdlib.h>
 #include <string.h>
 
+/* ---- FP8 E4M3 codec (src/quantization.cpp) ---------------------------- */
+
+/* compute_e4m3_to_float, src/quantization.cpp:25-48. */
+float orc_fp8_decode(uint8_t b) {
+    const int sign = (b >> 7) & 1, e = (b >> 3) & 0xF, m = b & 7;
+    if (e == 0xF) {
+        if (m == 6) return sign ? -INFINITY : INFINITY;
+        return NAN;
+    }
+    float v;
+    if (e == 0) v = (float)m / 8.0f * ldexpf(1.0f, -6);
+    else v = (1.0f + (float)m / 8.0f) * ldexpf(1.0f, e - 7);
+    return sign ? -v : v;
+}
+
+/* compute_float_to_e4m3, src/quantization.cpp:50-82 -- the encoder of the KV
+ * pool's write path (float_to_fp8_e4m3_batch, :183-188): the sign is v < 0
+ * (so -0.0 encodes as 0x00); scan every code of that sign and keep the first
+ * with the smallest |abs_v - |decode(code)|| (NaN errors never win). */
+uint8_t orc_fp8_encode(float v) {
+    if (isnan(v)) return 0xFF;
+    if (isinf(v)) return v > 0 ? 0x7E : 0xFE;
+    const int sign = v < 0 ? 1 : 0;
+    const float a = fabsf(v);
+    if (a == 0.0f) return (uint8_t)(sign << 7);
+    uint8_t best = 0;
+    float best_err = INFINITY;
+    for (int i = 0; i < 256; i++) {
+        if ((i >> 7) != sign) continue;
+        const float err = fabsf(a - fabsf(orc_fp8_decode((uint8_t)i)));
+        if (err < best_err) {
+            best_err = err;
+            best = (uint8_t)i;
+        }
+    }
+    return best;
+}
+
+void orc_fp8_encode_n(const float* x, uint8_t* b, int64_t n) {
+    for (int64_t i = 0; i < n; i++) b[i] = orc_fp8_encode(x[i]);
+}
+
+void orc_fp8_decode_n(const uint8_t* b, float* x, int64_t n) {
+    for (int64_t i = 0; i < n; i++) x[i] = orc_fp8_decode(b[i]);
+}
+
 /* ---- fp16 codec ------------------------------------------------------- */
 
 /* Reference fp32 -> fp16 encoder, src/kv_cache_manager.cpp:157-179:
@@ -133,6 +179,9 @@ static int load_row(const orc_pool* p, int which, int32_t block_id, int32_t tok,
     } else if (p->kind == ORC_F16) {
         const uint16_t* h = (const uint16_t*)base + off;
         for (int32_t d = 0; d < D; d++) row[d] = orc_f16_decode(h[d]);
+    } else if (p->kind == ORC_FP8) {
+        const uint8_t* c = (const uint8_t*)base + off;
+        for (int32_t d = 0; d < D; d++) row[d] = orc_fp8_decode(c[d]);
     } else {
         const int8_t* c = (const int8_t*)base + off;
         const uint16_t* sc = which ? p->v_scale : p->k_scale;

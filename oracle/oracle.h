@@ -24,10 +24,10 @@
 extern "C" {
 #endif
 
-enum { ORC_F32 = 0, ORC_F16 = 1, ORC_I8 = 2 };
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_I8 = 2, ORC_FP8 = 3 };
 
 typedef struct {
-    int32_t kind;              /* ORC_F32 / ORC_F16 / ORC_I8 */
+    int32_t kind;              /* ORC_F32 / ORC_F16 / ORC_I8 / ORC_FP8 */
     const void* k;             /* element base of block 0 */
     const void* v;
     const uint16_t* k_scale;   /* ORC_I8 only */
@@ -45,6 +45,15 @@ uint16_t orc_f16_encode_trunc(float x);
 float orc_f16_decode(uint16_t h);
 void orc_f16_encode_trunc_n(const float* x, uint16_t* h, int64_t n);
 void orc_f16_decode_n(const uint16_t* h, float* x, int64_t n);
+
+/* FP8 E4M3 codec of the reference KV pool (src/quantization.cpp:25-82,
+ * 176-188): bias 7, max finite 240, exponent 15 = inf (mantissa 6) or NaN; the
+ * encoder picks the nearest finite code of the value's sign (first, i.e.
+ * smaller, on a tie), inf -> 0x7E / 0xFE, NaN -> 0xFF, +0 and -0 -> 0x00. */
+float orc_fp8_decode(uint8_t b);
+uint8_t orc_fp8_encode(float v);
+void orc_fp8_encode_n(const float* x, uint8_t* b, int64_t n);
+void orc_fp8_decode_n(const uint8_t* b, float* x, int64_t n);
 
 /* Symmetric int8 quantiser per (token, kv head) vector of `d` values:
  * scale = fp16_rne(max|x| / 127); q = clamp(rne(x / float(scale)), -127, 127);

@@ -7,17 +7,25 @@
 // write fixtures, and bench.py time the reference as the CPU baseline.
 #include "paged_attention.h"
 #include "kv_cache_manager.h"
+#include "quantization.h"
 
 #include <cstdint>
 #include <vector>
 
 extern "C" {
 
-// dtype: 0 = KVDtype::FP32, 1 = KVDtype::FP16 (src/config.h:69-73).
+// dtype: 0 = KVDtype::FP32, 1 = KVDtype::FP16, 2 = KVDtype::FP8_E4M3
+// (src/config.h:69-73).
 void* ref_pool_create(int32_t num_blocks, int32_t num_layers, int32_t kv_dim, int32_t dtype) {
     return new KVCacheManager(num_layers, kv_dim, num_blocks,
-                              dtype == 1 ? KVDtype::FP16 : KVDtype::FP32);
+                              dtype == 1 ? KVDtype::FP16
+                                         : dtype == 2 ? KVDtype::FP8_E4M3 : KVDtype::FP32);
 }
+
+// The reference FP8 E4M3 codec of the KV pool's conversions
+// (src/kv_cache_manager.cpp:145-146,180-181 -> src/quantization.cpp:176-188).
+void ref_fp8_encode_n(const float* x, uint8_t* b, int64_t n) { float_to_fp8_e4m3_batch(x, b, n); }
+void ref_fp8_decode_n(const uint8_t* b, float* x, int64_t n) { fp8_e4m3_to_float_batch(b, x, n); }
 
 void ref_pool_destroy(void* m) { delete static_cast<KVCacheManager*>(m); }
 

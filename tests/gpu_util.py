@@ -3,9 +3,10 @@ import numpy as np
 import torch
 
 import pyvcpp
-from oracle_lib import ORC_F16, ORC_F32, ORC_I8
+from oracle_lib import ORC_F16, ORC_F32, ORC_FP8, ORC_I8
 
-KIND_TO_VCPP = {ORC_F32: pyvcpp.KV_F32, ORC_F16: pyvcpp.KV_F16, ORC_I8: pyvcpp.KV_I8}
+KIND_TO_VCPP = {ORC_F32: pyvcpp.KV_F32, ORC_F16: pyvcpp.KV_F16, ORC_I8: pyvcpp.KV_I8,
+                ORC_FP8: pyvcpp.KV_FP8}
 
 
 def dev(a, device="cuda:0"):

@@ -13,7 +13,7 @@ ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libref.so")
 REF_ENGINE_SO = os.path.join(ROOT, "oracle", "_ref", "libref_engine.so")
 
-ORC_F32, ORC_F16, ORC_I8 = 0, 1, 2
+ORC_F32, ORC_F16, ORC_I8, ORC_FP8 = 0, 1, 2, 3
 BS = 16  # reference BLOCK_SIZE (src/config.h:48)
 
 
@@ -57,6 +57,12 @@ def orc():
         L.orc_f16_encode_trunc_n.argtypes = [vp, vp, i64]
         L.orc_f16_decode_n.argtypes = [vp, vp, i64]
         L.orc_quant_i8.argtypes = [vp, i32, vp, vp]
+        L.orc_fp8_encode.argtypes = [ctypes.c_float]
+        L.orc_fp8_encode.restype = ctypes.c_uint8
+        L.orc_fp8_decode.argtypes = [ctypes.c_uint8]
+        L.orc_fp8_decode.restype = ctypes.c_float
+        L.orc_fp8_encode_n.argtypes = [vp, vp, i64]
+        L.orc_fp8_decode_n.argtypes = [vp, vp, i64]
         L.orc_quant_i8_rows.argtypes = [vp, i64, i32, vp, vp]
         L.orc_paged_attention.argtypes = [ctypes.POINTER(OrcPool), vp, vp, i32, i32, i32, vp]
         L.orc_decode_batch.argtypes = [ctypes.POINTER(OrcPool), vp, vp, i64, vp, vp, i32, i32,
@@ -91,6 +97,8 @@ def ref():
         L.ref_pool_destroy.argtypes = [vp]
         L.ref_pool_write.argtypes = [vp, i32, vp, vp]
         L.ref_pool_read_raw.argtypes = [vp, i32, vp, vp]
+        L.ref_fp8_encode_n.argtypes = [vp, vp, i64]
+        L.ref_fp8_decode_n.argtypes = [vp, vp, i64]
         L.ref_decode.argtypes = [vp, i32, vp, vp, i64, vp, vp, i32, i32, i32, i32, vp]
         L.ref_prefill.argtypes = [vp, i32, vp, vp, i64, vp, vp, i32, i32, i32, i32, vp]
         _ref = L
@@ -129,6 +137,20 @@ def f16_decode(h):
     h = np.ascontiguousarray(h, dtype=np.uint16)
     x = np.empty(h.shape, dtype=np.float32)
     orc().orc_f16_decode_n(_p(h), _p(x), h.size)
+    return x
+
+
+def fp8_encode(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    b = np.empty(x.shape, dtype=np.uint8)
+    orc().orc_fp8_encode_n(_p(x), _p(b), x.size)
+    return b
+
+
+def fp8_decode(b):
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    x = np.empty(b.shape, dtype=np.float32)
+    orc().orc_fp8_decode_n(_p(b), _p(x), b.size)
     return x
 
 
@@ -171,6 +193,8 @@ class Pool:
             return self.k.astype(np.float32), self.v.astype(np.float32)
         if self.kind == ORC_F16:
             return f16_decode(self.k), f16_decode(self.v)
+        if self.kind == ORC_FP8:
+            return fp8_decode(self.k), fp8_decode(self.v)
         ks = f16_decode(self.k_scale).transpose(0, 2, 1)[..., None]  # [nb][BS][Hkv][1]
         vs = f16_decode(self.v_scale).transpose(0, 2, 1)[..., None]
         return (self.k.astype(np.float32) * ks).astype(np.float32), \
@@ -185,6 +209,8 @@ def make_pool(kind, seed, num_blocks, num_kv_heads, head_dim, mean=0.0, std=1.0)
         return Pool(kind, k, v)
     if kind == ORC_F16:
         return Pool(kind, f16_trunc(k), f16_trunc(v))
+    if kind == ORC_FP8:
+        return Pool(kind, fp8_encode(k), fp8_encode(v))
     kq, ks = quant_i8(k)
     vq, vs = quant_i8(v)
     # scales [nb][BS][Hkv] -> [nb][Hkv][BS]
@@ -229,22 +255,22 @@ def single(pool, q, table, seq_len, num_heads):
 # ---- compiled reference ------------------------------------------------------
 
 class RefPool:
-    """A reference KVCacheManager (FP32 or FP16) filled through write_kv."""
+    """A reference KVCacheManager (FP32, FP16 or FP8_E4M3) filled through write_kv."""
 
-    def __init__(self, k, v, fp16):
+    def __init__(self, k, v, fp16=False, fp8=False):
         nb, bs, hkv, d = k.shape
         assert bs == BS
         self.kv_dim = hkv * d
         self.num_kv_heads, self.head_dim = hkv, d
-        self.h = ref().ref_pool_create(nb, 1, self.kv_dim, 1 if fp16 else 0)
+        self.h = ref().ref_pool_create(nb, 1, self.kv_dim, 2 if fp8 else 1 if fp16 else 0)
         k = np.ascontiguousarray(k, dtype=np.float32)
         v = np.ascontiguousarray(v, dtype=np.float32)
         ref().ref_pool_write(self.h, 0, _p(k), _p(v))
         self.shape = k.shape
-        self.fp16 = fp16
+        self.fp16, self.fp8 = fp16, fp8
 
     def raw(self):
-        dt = np.uint16 if self.fp16 else np.float32
+        dt = np.uint8 if self.fp8 else np.uint16 if self.fp16 else np.float32
         k = np.empty(self.shape, dtype=dt)
         v = np.empty(self.shape, dtype=dt)
         ref().ref_pool_read_raw(self.h, 0, _p(k), _p(v))

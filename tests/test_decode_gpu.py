@@ -2,7 +2,7 @@
 against the CPU oracle on identical seeded inputs.
 
 Tolerances (numpy allclose form, err <= atol + rtol * |want|):
-  fp32 KV: atol 1e-4, rtol 1e-4;  fp16 / int8 KV: atol 2e-3, rtol 1e-2.
+  fp32 KV: atol 1e-4, rtol 1e-4;  fp16 / int8 / fp8 KV: atol 2e-3, rtol 1e-2.
 """
 import numpy as np
 import pytest
@@ -14,7 +14,9 @@ from gpu_util import DevPool, assert_close, dev, gpu_decode
 
 pytestmark = pytest.mark.gpu
 
-TOL = {O.ORC_F32: (1e-4, 1e-4), O.ORC_F16: (2e-3, 1e-2), O.ORC_I8: (2e-3, 1e-2)}
+TOL = {O.ORC_F32: (1e-4, 1e-4), O.ORC_F16: (2e-3, 1e-2), O.ORC_I8: (2e-3, 1e-2),
+       O.ORC_FP8: (2e-3, 1e-2)}
+KINDS = [O.ORC_F32, O.ORC_F16, O.ORC_I8, O.ORC_FP8]
 
 
 def random_tables(seed, ctx, num_blocks, max_blocks=None):
@@ -39,7 +41,7 @@ def config1(kind=O.ORC_F32):
     return pool, q, table, np.array([512], dtype=np.int32)
 
 
-@pytest.mark.parametrize("kind", [O.ORC_F32, O.ORC_F16, O.ORC_I8])
+@pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("partition", [0, 64, 512])
 def test_config1(cuda, kind, partition):
     pool, q, table, ctx = config1(kind)
@@ -49,7 +51,7 @@ def test_config1(cuda, kind, partition):
 
 
 @pytest.mark.parametrize("partition", [64, 0])
-@pytest.mark.parametrize("kind", [O.ORC_F32, O.ORC_F16, O.ORC_I8])
+@pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("heads", [(1, 1), (8, 1), (64, 8), (12, 4), (32, 2), (32, 8)])
 def test_small_cases(cuda, kind, heads, partition):
     H, Hkv = heads
@@ -77,7 +79,7 @@ def test_other_head_dims(cuda, D, partition):
 
 
 @pytest.mark.parametrize("partition", [64, 0])
-@pytest.mark.parametrize("kind", [O.ORC_F32, O.ORC_F16, O.ORC_I8])
+@pytest.mark.parametrize("kind", KINDS)
 def test_skip_rules(cuda, kind, partition):
     """Invalid block ids and positions past the table are skipped, as the
     reference does (src/paged_attention.cpp:38,42)."""
@@ -219,3 +221,17 @@ def test_block_size_32(cuda):
     dp = DevPool(pool)
     got = gpu_decode(dp, q, tables, ctx, 64)
     assert_close(got, want, *TOL[O.ORC_F16], what="block size 32")
+
+
+@pytest.mark.parametrize("partition", [0, 128])
+@pytest.mark.parametrize("D", [64, 128])
+def test_fp8_other_head_dims(cuda, D, partition):
+    """FP8 pages (the reference KV_FP8 pool's E4M3 bytes) on the page-staged
+    kernel (D 64) and the register-path kernel (D 128, fixed partitions)."""
+    ctx = np.array([5, 48, 300, 1], dtype=np.int32)
+    pool = O.make_pool(O.ORC_FP8, 231, 40, 8, D, std=3.0)
+    q = O.normal(233, (4, 64, D))
+    tables = random_tables(239, ctx, 40)
+    want = O.decode(pool, q, tables, ctx, 64)
+    got = gpu_decode(DevPool(pool), q, tables, ctx, 64, partition_size=partition)
+    assert_close(got, want, *TOL[O.ORC_FP8], what="fp8 D=%d P=%d" % (D, partition))

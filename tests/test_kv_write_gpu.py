@@ -33,6 +33,8 @@ def empty_pool(kind):
         return O.Pool(kind, np.full(shape, 7.0, np.float32), np.full(shape, 7.0, np.float32))
     if kind == O.ORC_F16:
         return O.Pool(kind, np.full(shape, 0x1234, np.uint16), np.full(shape, 0x4321, np.uint16))
+    if kind == O.ORC_FP8:
+        return O.Pool(kind, np.full(shape, 0x5A, np.uint8), np.full(shape, 0xA5, np.uint8))
     sc = np.full((NB, HKV, BS), 0x3C00, np.uint16)
     return O.Pool(kind, np.full(shape, 5, np.int8), np.full(shape, -5, np.int8), sc, sc.copy())
 
@@ -47,11 +49,30 @@ def readback(dp, kind):
     return k, v, None, None
 
 
-@pytest.mark.parametrize("kind,rne", [(O.ORC_F32, 0), (O.ORC_F16, 0), (O.ORC_F16, 1), (O.ORC_I8, 0)])
+def fp8_rows(seed, n):
+    """Rows holding every E4M3 value, every midpoint between neighbours (ties
+    go to the smaller code), their float neighbours, and the values past 240
+    where the reference's float errors tie across codes (2^32 -> 144, from 2^33
+    -> 0)."""
+    x = O.normal(seed, (n, HKV, D), 0.0, 30.0).reshape(-1)
+    fin = np.sort(O.fp8_decode(np.arange(0x78, dtype=np.uint8)))
+    mids = ((fin[1:].astype(np.float64) + fin[:-1]) / 2).astype(np.float32)
+    sp = np.concatenate([fin, mids, np.nextafter(mids, np.float32(0)),
+                         np.nextafter(mids, np.float32(1e9)),
+                         np.array([240.0, 241.0, 300.0, 1e6, 2.0 ** 32, 2.0 ** 33, 1e30, 0.0, -0.0,
+                                   np.inf, -np.inf, np.nan, 1e-30, 2.0 ** -10], np.float32)])
+    sp = np.concatenate([sp, -sp]).astype(np.float32)
+    x[:sp.size] = sp
+    return x.reshape(n, HKV, D)
+
+
+@pytest.mark.parametrize("kind,rne", [(O.ORC_F32, 0), (O.ORC_F16, 0), (O.ORC_F16, 1), (O.ORC_I8, 0),
+                                      (O.ORC_FP8, 0)])
 def test_write_kv_bit_exact(cuda, kind, rne):
     n = 40
-    k = special_rows(71, n)
-    v = special_rows(72, n)
+    rows = fp8_rows if kind == O.ORC_FP8 else special_rows
+    k = rows(71, n)
+    v = rows(72, n)
     slots = O.permutation(73, NB * BS)[:n].astype(np.int64)
     slots[5] = -1                 # skipped
     slots[6] = NB * BS + 3        # block past the pool: skipped
@@ -73,6 +94,8 @@ def test_write_kv_bit_exact(cuda, kind, rne):
                 dst[b, p] = src
             elif kind == O.ORC_F16:
                 dst[b, p] = src.astype(np.float16).view(np.uint16) if rne else O.f16_trunc(src)
+            elif kind == O.ORC_FP8:
+                dst[b, p] = O.fp8_encode(src)
             else:
                 q, sc = O.quant_i8(src)
                 dst[b, p] = q
@@ -84,7 +107,7 @@ def test_write_kv_bit_exact(cuda, kind, rne):
         np.testing.assert_array_equal(gvs, wvs)
 
 
-@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8])
+@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8, O.ORC_FP8])
 def test_write_then_prefill(cuda, kind):
     """Pages written on the device from fp32 K/V, then a causal prefill over
     them, equal the oracle on pages the oracle encoded itself."""
@@ -100,6 +123,8 @@ def test_write_then_prefill(cuda, kind):
     shape = (nb, 16, Hkv, Dd)
     if kind == O.ORC_F16:
         host = O.Pool(kind, np.zeros(shape, np.uint16), np.zeros(shape, np.uint16))
+    elif kind == O.ORC_FP8:
+        host = O.Pool(kind, np.zeros(shape, np.uint8), np.zeros(shape, np.uint8))
     else:
         host = O.Pool(kind, np.zeros(shape, np.int8), np.zeros(shape, np.int8),
                       np.zeros((nb, Hkv, 16), np.uint16), np.zeros((nb, Hkv, 16), np.uint16))
@@ -112,6 +137,8 @@ def test_write_then_prefill(cuda, kind):
         b, p = divmod(int(s), 16)
         if kind == O.ORC_F16:
             host.k[b, p], host.v[b, p] = O.f16_trunc(k[t]), O.f16_trunc(v[t])
+        elif kind == O.ORC_FP8:
+            host.k[b, p], host.v[b, p] = O.fp8_encode(k[t]), O.fp8_encode(v[t])
         else:
             (host.k[b, p], host.k_scale[b, :, p]), (host.v[b, p], host.v_scale[b, :, p]) = \
                 O.quant_i8(k[t]), O.quant_i8(v[t])

@@ -318,3 +318,83 @@ def test_flash_attention_mask():
     for h in range(H):
         np.testing.assert_allclose(out[0, h], v[0, h, 5], atol=1e-6)
         assert abs(w[h, 5] - 1.0) < 1e-6 and np.all(w[h, np.arange(kv) != 5] == 0.0)
+
+
+# ---- FP8 E4M3 pages (src/quantization.cpp, the reference's KV_FP8 pool) ----
+
+def test_fp8_decode_known_values():
+    # bias 7, 3 mantissa bits; 0x77 = 1.875 * 2^7 = 240; exponent 15 = inf/NaN
+    known = {0x00: 0.0, 0x01: 2.0 ** -9, 0x07: 7 * 2.0 ** -9, 0x08: 2.0 ** -6, 0x38: 1.0,
+             0x39: 1.125, 0x3F: 1.875, 0x40: 2.0, 0x77: 240.0, 0xB8: -1.0, 0xF7: -240.0}
+    for b, v in known.items():
+        assert O.fp8_decode(np.array([b], np.uint8))[0] == np.float32(v), hex(b)
+    sp = O.fp8_decode(np.array([0x7E, 0xFE, 0x7F, 0xFF, 0x78, 0x7D], np.uint8))
+    assert sp[0] == np.inf and sp[1] == -np.inf and np.all(np.isnan(sp[2:]))
+
+
+def test_fp8_encode_known_answers():
+    x = np.array([1.0, 1.0625, 1.0625001, 1.1875, 240.0, 250.0, 2.0 ** 32, 2.0 ** 34, 1e30,
+                  np.inf, -np.inf, np.nan, -0.0, 0.0, 2.0 ** -10, 2.0 ** -10 * 1.0001,
+                  3 * 2.0 ** -10, -1.5, 0.015625, -1e30], np.float32)
+    want = [0x38,
+            0x38,  # 1.0625: halfway between 1.0 and 1.125, the first (smaller) code wins
+            0x39,
+            0x39,  # 1.1875: halfway between 1.125 and 1.25
+            0x77, 0x77,  # saturate at 240
+            0x71,  # 2^32: fl(a - v) is the same for v in [144, 240], the first such code wins
+            0x00, 0x00,  # from 2^33, fl(a - v) == a for every code: code 0 wins
+            0x7E, 0xFE, 0xFF,
+            0x00,  # -0.0: the write path takes the sign from v < 0
+            0x00, 0x00, 0x01, 0x01, 0xBC, 0x08,
+            0x80]  # the first code of the negative half is -0
+    got = O.fp8_encode(x)
+    assert [hex(v) for v in got] == [hex(v) for v in want]
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built")
+def test_fp8_codec_matches_reference():
+    """Every code decodes as the reference pool decodes it; the encoder agrees
+    with the reference's write path on every code's value, every midpoint
+    between neighbours (the tie rule), their float neighbours, specials and a
+    log-uniform sweep."""
+    L = O.ref()
+    codes = np.arange(256, dtype=np.uint8)
+    want = np.empty(256, np.float32)
+    L.ref_fp8_decode_n(O._p(codes), O._p(want), 256)
+    np.testing.assert_array_equal(O.fp8_decode(codes), want)
+    fin = np.sort(want[np.isfinite(want) & (want >= 0)])
+    mids = ((fin[1:].astype(np.float64) + fin[:-1]) / 2).astype(np.float32)
+    xs = np.concatenate([fin, mids, np.nextafter(mids, np.float32(0)), np.nextafter(mids, np.float32(1e9)),
+                         np.array([245.0, 248.0, 256.0, 1e10, 2.0 ** 32, 2.0 ** 33, 2.0 ** 33 + 2048,
+                                   2.0 ** -12, 1e-30, 0.0, np.inf, np.nan], np.float32),
+                         np.exp(np.random.default_rng(1).uniform(-12, 7, 20000)).astype(np.float32)])
+    xs = np.concatenate([xs, -xs]).astype(np.float32)
+    ref_b = np.empty(xs.shape, np.uint8)
+    L.ref_fp8_encode_n(O._p(xs), O._p(ref_b), xs.size)
+    np.testing.assert_array_equal(O.fp8_encode(xs), ref_b)
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built")
+def test_fp8_pool_attention_matches_reference():
+    """The reference's own FP8_E4M3 pool (write_kv encodes, get_k decodes)
+    against the oracle's FP8 pool: identical pages, identical outputs."""
+    nb, hkv, D, H = 40, 8, 80, 64
+    k = O.normal(71, (nb, O.BS, hkv, D), std=2.0)
+    v = O.normal(72, (nb, O.BS, hkv, D), std=2.0)
+    rp = O.RefPool(k, v, fp8=True)
+    rk, rv = rp.raw()
+    pool = O.make_pool(O.ORC_FP8, 71, nb, hkv, D, std=2.0)
+    np.testing.assert_array_equal(pool.k, rk)
+    np.testing.assert_array_equal(pool.v, rv)
+    ctx = np.array([1, 17, 100, 200], np.int32)
+    perm = O.permutation(73, nb)
+    tables = np.full((4, 13), -1, np.int32)
+    off = 0
+    for i, c in enumerate(ctx):
+        n = (c + O.BS - 1) // O.BS
+        tables[i, :n] = perm[off:off + n]
+        off += n
+    q = O.normal(74, (4, H, D))
+    # the reference build contracts to FMA (see test_live_reference_decode)
+    np.testing.assert_allclose(O.decode(pool, q, tables, ctx, H), rp.decode(q, tables, ctx, H),
+                               atol=1e-6, rtol=1e-5)

@@ -1,7 +1,7 @@
 """GPU parity of the chunked causal prefill path (vcpp_paged_prefill) against
 the CPU oracle's per-position semantics on identical seeded inputs.
 
-Tolerance (numpy allclose form): atol 2e-3, rtol 1e-2 for fp16 and int8 pages.
+Tolerance (numpy allclose form): atol 2e-3, rtol 1e-2 for fp16, int8 and fp8 pages.
 q is fp16 on the GPU; the oracle gets the same fp16 values as fp32.
 """
 import numpy as np
@@ -26,7 +26,7 @@ def make_case(kind, seed, prefix, chunk, H, Hkv, D=80, std=1.0, extra_blocks=8):
     return pool, q16, q16.astype(np.float32), tables, q_start, np.array(prefix, np.int32)
 
 
-@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8])
+@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8, O.ORC_FP8])
 @pytest.mark.parametrize("heads", [(64, 8), (8, 1), (32, 2), (16, 16)])
 def test_prefill_small(cuda, kind, heads):
     H, Hkv = heads
@@ -38,7 +38,7 @@ def test_prefill_small(cuda, kind, heads):
     assert_close(got, want, ATOL, RTOL, what="prefill H=%d Hkv=%d kind=%d" % (H, Hkv, kind))
 
 
-@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8])
+@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8, O.ORC_FP8])
 @pytest.mark.parametrize("D", [64, 128])
 def test_prefill_head_dims(cuda, D, kind):
     prefix, chunk = [7, 100], [90, 33]
@@ -48,7 +48,7 @@ def test_prefill_head_dims(cuda, D, kind):
     assert_close(got, want, ATOL, RTOL, what="prefill D=%d kind=%d" % (D, kind))
 
 
-@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8])
+@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8, O.ORC_FP8])
 def test_prefill_skips_invalid_blocks(cuda, kind):
     prefix, chunk = [48, 0], [40, 70]
     pool, q16, q32, tables, q_start, pre = make_case(kind, 620, prefix, chunk, 64, 8)
@@ -59,7 +59,7 @@ def test_prefill_skips_invalid_blocks(cuda, kind):
     assert_close(got, want, ATOL, RTOL, what="prefill invalid blocks kind=%d" % kind)
 
 
-@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8])
+@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8, O.ORC_FP8])
 @pytest.mark.parametrize("D", [64, 80, 128])
 def test_prefill_long_prefix(cuda, kind, D):
     """Prefixes of several hundred 32-key blocks: many trips round the K/V

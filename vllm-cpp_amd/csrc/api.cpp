@@ -101,14 +101,16 @@ DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_he
     const int groups = vcpp::decode_group_count(pairs);
     // The page-staged kernel (balanced split only) unless VCPP_DECODE_PAGE=0.
     const char* pe = getenv("VCPP_DECODE_PAGE");
-    // Its 16-byte DMA of int8 pages and scales needs 16-byte aligned bases and
-    // strides (fp16 pages already must be).
+    // Its 16-byte DMA of byte pages (and int8 scales) needs 16-byte aligned
+    // bases and strides (fp16 pages already must be).
+    const bool bytes = kv->dtype == VCPP_KV_I8 || kv->dtype == VCPP_KV_FP8;
     const bool dma_aligned =
-        kv->dtype != VCPP_KV_I8 ||
-        (kv->block_stride % 16 == 0 && kv->scale_block_stride % 8 == 0 &&
-         reinterpret_cast<uintptr_t>(kv->k) % 16 == 0 && reinterpret_cast<uintptr_t>(kv->v) % 16 == 0 &&
-         reinterpret_cast<uintptr_t>(kv->k_scale) % 16 == 0 &&
-         reinterpret_cast<uintptr_t>(kv->v_scale) % 16 == 0);
+        !bytes ||
+        (kv->block_stride % 16 == 0 && reinterpret_cast<uintptr_t>(kv->k) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(kv->v) % 16 == 0 &&
+         (kv->dtype != VCPP_KV_I8 ||
+          (kv->scale_block_stride % 8 == 0 && reinterpret_cast<uintptr_t>(kv->k_scale) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(kv->v_scale) % 16 == 0)));
     pl.page_mode = partition_size == 0 && !(pe && pe[0] == '0') && dma_aligned &&
                    vcpp::decode_page_mode_supported(kv->dtype, kv->num_kv_heads, group, D,
                                                     kv->block_size);
@@ -133,7 +135,8 @@ DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_he
 
 int check_pages(const vcpp_kv_pages* kv) {
     if (!kv) return fail(VCPP_E_INVALID, "kv pages descriptor is NULL");
-    if (kv->dtype != VCPP_KV_F32 && kv->dtype != VCPP_KV_F16 && kv->dtype != VCPP_KV_I8)
+    if (kv->dtype != VCPP_KV_F32 && kv->dtype != VCPP_KV_F16 && kv->dtype != VCPP_KV_I8 &&
+        kv->dtype != VCPP_KV_FP8)
         return fail(VCPP_E_INVALID, "unknown kv dtype %d", kv->dtype);
     if (kv->block_size <= 0 || kv->block_size % 16 != 0)
         return fail(VCPP_E_UNSUPPORTED, "block_size %d is not a positive multiple of 16",
@@ -146,7 +149,7 @@ int check_pages(const vcpp_kv_pages* kv) {
     if (kv->num_blocks > 0 && (!kv->k || !kv->v))
         return fail(VCPP_E_INVALID, "K/V page base is NULL");
     const int64_t esize = kv->dtype == VCPP_KV_F32 ? 4 : kv->dtype == VCPP_KV_F16 ? 2 : 1;
-    const int64_t align = kv->dtype == VCPP_KV_I8 ? 8 : 16;
+    const int64_t align = esize == 1 ? 8 : 16;
     if ((kv->block_stride * esize) % align != 0 || (kv->head_dim * esize) % align != 0 ||
         (reinterpret_cast<uintptr_t>(kv->k) % align) != 0 ||
         (reinterpret_cast<uintptr_t>(kv->v) % align) != 0)
@@ -343,7 +346,7 @@ int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
     int rc = check_pages(kv);
     if (rc != VCPP_OK) return rc;
     if (kv->dtype == VCPP_KV_F32)
-        return fail(VCPP_E_UNSUPPORTED, "prefill supports fp16 and int8 pages (got fp32)");
+        return fail(VCPP_E_UNSUPPORTED, "prefill supports fp16, int8 and fp8 pages (got fp32)");
     if (kv->head_dim != 64 && kv->head_dim != 80 && kv->head_dim != 128)
         return fail(VCPP_E_UNSUPPORTED, "prefill head_dim %d (64, 80 or 128)", kv->head_dim);
     if (num_chunks < 0 || max_chunk_len < 0)
@@ -398,7 +401,8 @@ int vcpp_write_kv(const vcpp_kv_pages* kv, const float* k, const float* v, const
     g_last_error.clear();
     // Writing needs less than attention: any head split and block size.
     if (!kv) return fail(VCPP_E_INVALID, "kv pages descriptor is NULL");
-    if (kv->dtype != VCPP_KV_F32 && kv->dtype != VCPP_KV_F16 && kv->dtype != VCPP_KV_I8)
+    if (kv->dtype != VCPP_KV_F32 && kv->dtype != VCPP_KV_F16 && kv->dtype != VCPP_KV_I8 &&
+        kv->dtype != VCPP_KV_FP8)
         return fail(VCPP_E_INVALID, "unknown kv dtype %d", kv->dtype);
     if (kv->block_size <= 0 || kv->num_kv_heads <= 0 || kv->head_dim <= 0 || kv->num_blocks < 0)
         return fail(VCPP_E_INVALID, "bad page shape");

@@ -90,6 +90,14 @@ struct Tile<VCPP_KV_I8, D> {
     i2 vs;  // fp16 V scales of tokens 4g..4g+3
 };
 
+template <int D>
+struct Tile<VCPP_KV_FP8, D> {
+    i2 k[Dims<D>::NC32 > 0 ? Dims<D>::NC32 : 1];
+    uint32_t kr;
+    i2 v[Dims<D>::NC32 > 0 ? Dims<D>::NC32 : 1];
+    uint32_t vr;
+};
+
 // Per-lane byte offsets of the lane's share of a tile, identical for every
 // tile: only the buffer base moves.
 struct LaneOffsets {
@@ -150,6 +158,8 @@ __device__ __forceinline__ void load_tile(Tile<KV, D>& t, const DecodeParams& p,
             t.kr = __builtin_amdgcn_raw_buffer_load_b32(kr, lo.rem, 0, 0);
             t.vr = __builtin_amdgcn_raw_buffer_load_b32(vr, lo.rem, 0, 0);
         }
+    }
+    if constexpr (KV == VCPP_KV_I8) {
         const int64_t se = (int64_t)(ok ? bid : 0) * p.scale_block_stride + tok_in_block;
         const int sbytes = ok ? (p.num_kv_heads * p.block_size - tok_in_block) * 2 : 0;
         const auto ksr = make_rsrc(p.k_scale + se, sbytes);
@@ -163,12 +173,12 @@ __device__ __forceinline__ void load_tile(Tile<KV, D>& t, const DecodeParams& p,
 template <int KV, int D>
 __device__ __forceinline__ h8 k_chunk(const Tile<KV, D>& t, int cc) {
     if constexpr (KV == VCPP_KV_F16) return t.k[cc];
-    else return i8x8_to_h8((uint32_t)t.k[cc].x, (uint32_t)t.k[cc].y);
+    else return bytes8_to_h8<KV>((uint32_t)t.k[cc].x, (uint32_t)t.k[cc].y);
 }
 template <int KV, int D>
 __device__ __forceinline__ h4 k_rem(const Tile<KV, D>& t) {
     if constexpr (KV == VCPP_KV_F16) return t.kr;
-    else return i8x4_to_h4(t.kr);
+    else return bytes4_to_h4<KV>(t.kr);
 }
 
 // Writes the lane's V row chunk (token c) into the wave's row-major LDS tile
@@ -183,14 +193,14 @@ __device__ __forceinline__ void stage_v(lds_char* tile, const Tile<KV, D>& t, bo
     for (int cc = 0; cc < NC32; ++cc) {
         h8 x;
         if constexpr (KV == VCPP_KV_F16) x = t.v[cc];
-        else x = i8x8_to_h8((uint32_t)t.v[cc].x, (uint32_t)t.v[cc].y);
+        else x = bytes8_to_h8<KV>((uint32_t)t.v[cc].x, (uint32_t)t.v[cc].y);
         if (!valid) x = h8{};
         *reinterpret_cast<__attribute__((address_space(3))) h8*>(row + (32 * cc + 8 * g) * 2) = x;
     }
     if constexpr (Dims<D>::REM) {
         h4 x;
         if constexpr (KV == VCPP_KV_F16) x = t.vr;
-        else x = i8x4_to_h4(t.vr);
+        else x = bytes4_to_h4<KV>(t.vr);
         if (!valid) x = h4{};
         *reinterpret_cast<__attribute__((address_space(3))) h4*>(row + (32 * NC32 + 4 * g) * 2) = x;
     }
@@ -773,11 +783,12 @@ __global__ __launch_bounds__(256) void merge_parts_kernel(DecodeParams p) {
 // head and writes complete sequences or (m, l, o) partials for
 // merge_split_kernel.
 //
-// int8 pages: the tile's 8 x 16 K scales and V scales (fp16, [head][token])
-// ride in one more DMA instruction.  K fragments are widened to exact fp16
-// integers in registers and their scale multiplies the fp32 score; each wave
-// widens its head's V rows into a private fp16 tile for the transposing reads,
-// and the V scale multiplies fp32 P before its fp16 split.
+// int8 and FP8 pages (one byte per value): K fragments are widened to fp16 in
+// registers (int8: exact integers; FP8: its values) and each wave widens its
+// head's V rows into a private fp16 tile for the transposing reads.  int8
+// pages also carry the tile's 8 x 16 K and V scales (fp16, [head][token]) in
+// one more DMA instruction: the K scale multiplies the fp32 score, the V scale
+// fp32 P before its fp16 split.
 
 constexpr int kPageWaves = 8;      // kv heads per workgroup (Hkv)
 constexpr int kPageWindow = 512;   // tiles listed in LDS at a time
@@ -794,21 +805,22 @@ struct PageEntry {
 
 template <int KV, int D>
 struct PageCfg {
-    static constexpr bool I8 = KV == VCPP_KV_I8;
-    static constexpr int ES = I8 ? 1 : 2;
+    static constexpr bool BYTES = KV != VCPP_KV_F16;   // int8 or FP8: one byte per value
+    static constexpr bool SCALED = KV == VCPP_KV_I8;   // per-(token, head) fp16 scales
+    static constexpr int ES = BYTES ? 1 : 2;
     static constexpr int RC = kPageWaves * D * ES / 16;   // 16-byte chunks per token row
     static constexpr int HC = D * ES / 16;                // chunks of one head in a row
     static constexpr int SWZ = RC % 16 == 0 ? 16 : 8;     // swizzle group (chunks)
     static constexpr int REG = 16 * RC * 16;              // bytes of one region (K or V) of a tile
     static constexpr int NI = REG / 1024;                 // DMA instructions per region
-    static constexpr int NREAL = 2 * NI + (I8 ? 1 : 0);   // + the scale instruction
+    static constexpr int NREAL = 2 * NI + (SCALED ? 1 : 0);  // + the scale instruction
     static constexpr int PERW = (NREAL + kPageWaves - 1) / kPageWaves;
-    static constexpr int STAGE = 2 * REG + (I8 ? 1024 : 0);
-    // int8 tiles carry half the bytes: twice the tiles in flight.
-    static constexpr int STAGES = I8 ? 5 : 3;
+    static constexpr int STAGE = 2 * REG + (SCALED ? 1024 : 0);
+    // byte tiles carry half the bytes: twice the tiles in flight.
+    static constexpr int STAGES = BYTES ? 5 : 3;
     static constexpr int OFF_JUNK = STAGES * STAGE;       // target of padding DMAs
     static constexpr int OFF_VT = OFF_JUNK + (PERW * kPageWaves > NREAL ? 1024 : 0);
-    static constexpr int OFF_LIST = OFF_VT + (I8 ? kPageWaves * 16 * D * 2 : 0);
+    static constexpr int OFF_LIST = OFF_VT + (BYTES ? kPageWaves * 16 * D * 2 : 0);
     static constexpr int LDS = OFF_LIST + kPageWindow * (int)sizeof(PageEntry);
     static_assert(RC % SWZ == 0 && REG % 1024 == 0 && (D * ES) % 16 == 0, "tile shape");
     static_assert(LDS <= 160 * 1024, "LDS budget");
@@ -839,7 +851,7 @@ template <int KV, int D>
 __global__ __launch_bounds__(kPageWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void decode_page_kernel(DecodeParams p) {
     using C = PageCfg<KV, D>;
-    constexpr bool I8 = C::I8;
+    constexpr bool BYTES = C::BYTES, SCALED = C::SCALED;
     constexpr int NC32 = Dims<D>::NC32, NT = Dims<D>::NT;
     constexpr int HKV = kPageWaves;
     constexpr int RC = C::RC, HC = C::HC, SWZ = C::SWZ, REG = C::REG, NI = C::NI;
@@ -906,7 +918,7 @@ void decode_page_kernel(DecodeParams p) {
                 const void* src = bid >= 0 ? (const void*)(base + elem * C::ES + (int64_t)gcn * 16)
                                            : (const void*)kZeroChunk16;
                 dma16_page(src, __builtin_amdgcn_readfirstlane(sbase + which * REG + (j - which * NI) * 1024));
-            } else if (I8 && j == 2 * NI) {
+            } else if (SCALED && j == 2 * NI) {
                 // lanes 0..15: K scales of head lane/2 (32 B = 2 chunks), 16..31: V scales
                 const int head = (lane >> 1) & 7, half = lane & 1;
                 const uint16_t* sp = lane >= 16 ? p.v_scale : p.k_scale;
@@ -1011,7 +1023,7 @@ void decode_page_kernel(DecodeParams p) {
     };
     typedef __attribute__((address_space(3))) uint32_t lds_u32;
     typedef __attribute__((address_space(3))) i2 lds_i2;
-    lds_char* vt = lds + C::OFF_VT + wave * 16 * D * 2;  // int8: this wave's fp16 V tile
+    lds_char* vt = lds + C::OFF_VT + wave * 16 * D * 2;  // byte pages: this wave's fp16 V tile
 
     auto compute_tile = [&](int tau, const PageEntry& e) {
         lds_char* sb = lds + (tau % STAGES) * STAGE;
@@ -1019,31 +1031,33 @@ void decode_page_kernel(DecodeParams p) {
         const bool full = e.bid >= 0 && pos0 + kTile <= cur_end;  // uniform
         f4 acc = {0.f, 0.f, 0.f, 0.f};
         i2 ksw = {}, vsw = {};
-        if constexpr (I8) {
-            // K scales of tokens 4g..4g+3 (head kvh), V scales likewise
-            ksw = *reinterpret_cast<lds_i2*>(sb + 2 * REG + kvh * 32 + 8 * g);
-            vsw = *reinterpret_cast<lds_i2*>(sb + 2 * REG + 256 + kvh * 32 + 8 * g);
+        if constexpr (BYTES) {
+            if constexpr (SCALED) {
+                // K scales of tokens 4g..4g+3 (head kvh), V scales likewise
+                ksw = *reinterpret_cast<lds_i2*>(sb + 2 * REG + kvh * 32 + 8 * g);
+                vsw = *reinterpret_cast<lds_i2*>(sb + 2 * REG + 256 + kvh * 32 + 8 * g);
+            }
 #pragma unroll
             for (int cc = 0; cc < NC32; ++cc) {
                 const i2 kw = *reinterpret_cast<lds_i2*>(sb + kofs(2 * cc + (g >> 1)) + 8 * (g & 1));
-                acc = mfma32(i8x8_to_h8((uint32_t)kw.x, (uint32_t)kw.y), qa[cc], acc);
+                acc = mfma32(bytes8_to_h8<KV>((uint32_t)kw.x, (uint32_t)kw.y), qa[cc], acc);
             }
             if constexpr (Dims<D>::REM) {
                 const uint32_t kw = *reinterpret_cast<lds_u32*>(sb + kofs(2 * NC32) + 4 * g);
                 const f4 zero = {0.f, 0.f, 0.f, 0.f};
-                acc += mfma16(i8x4_to_h4(kw), qr, zero);
+                acc += mfma16(bytes4_to_h4<KV>(kw), qr, zero);
             }
             // widen V rows of token c into the wave's row-major [16][D] fp16 tile
 #pragma unroll
             for (int cc = 0; cc < NC32; ++cc) {
                 const i2 vw = *reinterpret_cast<lds_i2*>(sb + REG + kofs(2 * cc + (g >> 1)) + 8 * (g & 1));
                 *reinterpret_cast<__attribute__((address_space(3))) h8*>(vt + (c * D + 32 * cc + 8 * g) * 2) =
-                    i8x8_to_h8((uint32_t)vw.x, (uint32_t)vw.y);
+                    bytes8_to_h8<KV>((uint32_t)vw.x, (uint32_t)vw.y);
             }
             if constexpr (Dims<D>::REM) {
                 const uint32_t vw = *reinterpret_cast<lds_u32*>(sb + REG + kofs(2 * NC32) + 4 * g);
                 *reinterpret_cast<__attribute__((address_space(3))) h4*>(vt + (c * D + 32 * NC32 + 4 * g) * 2) =
-                    i8x4_to_h4(vw);
+                    bytes4_to_h4<KV>(vw);
             }
         } else {
 #pragma unroll
@@ -1064,7 +1078,7 @@ void decode_page_kernel(DecodeParams p) {
         for (int r = 0; r < 4; ++r) {
             float x = acc[r] + dpp_ror8(acc[r]);
             float f = p.scale_log2;
-            if constexpr (I8) {
+            if constexpr (SCALED) {
                 const uint32_t wd = (uint32_t)(r < 2 ? ksw.x : ksw.y);
                 f *= h_to_f((r & 1) ? (wd >> 16) : (wd & 0xFFFFu));
             }
@@ -1092,7 +1106,7 @@ void decode_page_kernel(DecodeParams p) {
         for (int r = 0; r < 4; ++r) {
             float pr = fast_exp2(sc[r] - m_new);
             lsum += pr;
-            if constexpr (I8) {
+            if constexpr (SCALED) {
                 const uint32_t wd = (uint32_t)(r < 2 ? vsw.x : vsw.y);
                 // masked tokens have pr == 0; the select keeps 0 * garbage out
                 pr = pr > 0.f ? pr * h_to_f((r & 1) ? (wd >> 16) : (wd & 0xFFFFu)) : 0.f;
@@ -1103,7 +1117,7 @@ void decode_page_kernel(DecodeParams p) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             h4 vf;
-            if constexpr (I8) {
+            if constexpr (BYTES) {
                 vf = read_v_tr<D>(vt, t, g, c);
             } else {
                 const s4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -1261,11 +1275,16 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
         if (p.kv_dtype == VCPP_KV_I8)
             err = p.head_dim == 64 ? launch_page<VCPP_KV_I8, 64>(p, stream)
                                    : launch_page<VCPP_KV_I8, 80>(p, stream);
+        else if (p.kv_dtype == VCPP_KV_FP8)
+            err = p.head_dim == 64 ? launch_page<VCPP_KV_FP8, 64>(p, stream)
+                                   : launch_page<VCPP_KV_FP8, 80>(p, stream);
         else
             err = p.head_dim == 64 ? launch_page<VCPP_KV_F16, 64>(p, stream)
                                    : launch_page<VCPP_KV_F16, 80>(p, stream);
     } else if (p.kv_dtype == VCPP_KV_F16) {
         VCPP_DISPATCH_D(VCPP_KV_F16)
+    } else if (p.kv_dtype == VCPP_KV_FP8) {
+        VCPP_DISPATCH_D(VCPP_KV_FP8)
     } else {
         VCPP_DISPATCH_D(VCPP_KV_I8)
     }
@@ -1286,7 +1305,8 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
 
 bool decode_page_mode_supported(int kv_dtype, int num_kv_heads, int group, int head_dim,
                                 int block_size) {
-    return (kv_dtype == VCPP_KV_F16 || kv_dtype == VCPP_KV_I8) && num_kv_heads == kPageWaves &&
+    return (kv_dtype == VCPP_KV_F16 || kv_dtype == VCPP_KV_I8 || kv_dtype == VCPP_KV_FP8) &&
+           num_kv_heads == kPageWaves &&
            group <= 8 &&
            (head_dim == 64 || head_dim == 80) && block_size % kTile == 0;
 }

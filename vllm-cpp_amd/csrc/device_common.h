@@ -12,6 +12,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "vcpp_attention.h"
+
 namespace vcpp {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -69,5 +71,32 @@ __device__ __forceinline__ h4 i8x4_to_h4(uint32_t x) {
     const h4 bias = {1152, 1152, 1152, 1152};
     return v - bias;
 }
+
+// FP8 E4M3 bytes -> fp16 with the gfx950 converter (OCP E4M3, scale 1).  The
+// reference's E4M3 (bias 7, max 240) has the same value for every code whose
+// exponent field is below 15, so finite reference pages convert exactly.
+__device__ __forceinline__ h4 fp8x4_to_h4(uint32_t x) {
+    const h2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, false);
+    const h2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, true);
+    return h4{a[0], a[1], b[0], b[1]};
+}
+
+__device__ __forceinline__ h8 fp8x8_to_h8(uint32_t lo, uint32_t hi) {
+    const h4 a = fp8x4_to_h4(lo), b = fp8x4_to_h4(hi);
+    return h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Bytes of a KV page -> fp16 MFMA operands (int8: exact integers; FP8: values).
+template <int KV>
+__device__ __forceinline__ h8 bytes8_to_h8(uint32_t lo, uint32_t hi) {
+    if constexpr (KV == VCPP_KV_FP8) return fp8x8_to_h8(lo, hi);
+    else return i8x8_to_h8(lo, hi);
+}
+template <int KV>
+__device__ __forceinline__ h4 bytes4_to_h4(uint32_t x) {
+    if constexpr (KV == VCPP_KV_FP8) return fp8x4_to_h4(x);
+    else return i8x4_to_h4(x);
+}
+
 
 }  // namespace vcpp

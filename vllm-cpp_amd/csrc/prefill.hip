@@ -93,22 +93,22 @@ __device__ __forceinline__ int slot_of(int chunk, int key) { return chunk * kKBl
 // int8 pages: raw K/V chunks ([chunk of 16 dims][32 keys], 16 bytes per
 // slot, K region then V region) and the 32 + 32 fp16 scales of the block (one
 // dword per lane), dequantised by the workgroup into fp16 DmaDims stages.
-template <int D>
-struct I8Dims {
-    static constexpr int NCH = D / 16;             // 16-byte int8 chunks per row
+template <int D, bool SCALED>
+struct ByteDims {
+    static constexpr int NCH = D / 16;             // 16-byte chunks of one byte per value per row
     static constexpr int REGION = kKBlk * NCH;     // slots of K (or V)
     static constexpr int NDATA = 2 * REGION / 64;  // data DMA instructions per block
-    static constexpr int NINST = NDATA + 1;        // + one for the scales
+    static constexpr int NINST = NDATA + (SCALED ? 1 : 0);  // int8: + one for the scales
     static constexpr int PERW = (NINST + 3) / 4;
     static constexpr int SCALES = 2 * REGION * 16; // offset of the scale dwords
-    static constexpr int STAGE = SCALES + 64 * 4;
+    static constexpr int STAGE = SCALES + (SCALED ? 64 * 4 : 0);
     static constexpr int STAGES = D <= 80 ? 8 : 4; // ring depth
-    static constexpr int UNITS = 2 * REGION;       // dequant units (16 dims) per block
-    static_assert((2 * REGION) % 64 == 0, "int8 stage must be whole DMA instructions");
+    static constexpr int UNITS = 2 * REGION;       // widening units (16 values) per block
+    static_assert((2 * REGION) % 64 == 0, "byte stage must be whole DMA instructions");
 };
 
-// Query row blocks per wave: 4 (2 for D = 128) with fp16 pages; int8 pages
-// carry per-key scale state and use 2.
+// Query row blocks per wave: 4 (2 for D = 128) with fp16 and FP8 pages; int8
+// pages carry per-key scale state and use 2.
 template <int KV, int D>
 constexpr int rows_blocks() { return KV == VCPP_KV_I8 ? 2 : PDims<D>::RB; }
 
@@ -159,22 +159,23 @@ template <int KV, int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_dma_kernel(PrefillParams p) {
     using DD = DmaDims<D>;
-    using ID = I8Dims<D>;
-    constexpr bool I8 = KV == VCPP_KV_I8;
+    constexpr bool BYTES = KV != VCPP_KV_F16;  // int8 / FP8: byte ring widened to fp16
+    constexpr bool SCALED = KV == VCPP_KV_I8;  // per-key fp16 scales
+    using ID = ByteDims<D, SCALED>;
     // LDS: the DMA ring (fp16 stages, or int8 stages plus an fp16 area of two
     // dequantised blocks), then the tile's block table.
-    constexpr int kStages = I8 ? ID::STAGES : DD::STAGES;
-    constexpr int RSTAGE = I8 ? ID::STAGE : DD::STAGE;
+    constexpr int kStages = BYTES ? ID::STAGES : DD::STAGES;
+    constexpr int RSTAGE = BYTES ? ID::STAGE : DD::STAGE;
     constexpr int AREA = kStages * RSTAGE;
-    constexpr int NF16 = I8 ? 2 : kStages;       // fp16-format stages
-    constexpr int F16BASE = I8 ? AREA : 0;
+    constexpr int NF16 = BYTES ? 2 : kStages;       // fp16-format stages
+    constexpr int F16BASE = BYTES ? AREA : 0;
     constexpr int SG = 2;  // row blocks per softmax group
     constexpr int NC32 = PDims<D>::NC32, NT = PDims<D>::NT;
     constexpr int RB = rows_blocks<KV, D>();  // 16-row blocks per wave
     constexpr int kQTile = 16 * RB;
     extern __shared__ __attribute__((aligned(16))) char smem[];
     lds_char* lds = reinterpret_cast<lds_char*>((__attribute__((address_space(3))) char*)smem);
-    int32_t* table_s = reinterpret_cast<int32_t*>(smem + AREA + (I8 ? 2 * DD::STAGE : 0));
+    int32_t* table_s = reinterpret_cast<int32_t*>(smem + AREA + (BYTES ? 2 * DD::STAGE : 0));
     const uint32_t lds_addr = (uint32_t)(uintptr_t)lds;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -330,8 +331,8 @@ void prefill_dma_kernel(PrefillParams p) {
                 const int ch = q >> 5, key = q & 31;
                 lds_char* st = lds + ((kb + blk) % kStages) * RSTAGE;
                 const i4 raw = *reinterpret_cast<__attribute__((address_space(3))) i4*>(st + v * 16);
-                const h8 lo = i8x8_to_h8((uint32_t)raw.x, (uint32_t)raw.y);
-                const h8 hi = i8x8_to_h8((uint32_t)raw.z, (uint32_t)raw.w);
+                const h8 lo = bytes8_to_h8<KV>((uint32_t)raw.x, (uint32_t)raw.y);
+                const h8 hi = bytes8_to_h8<KV>((uint32_t)raw.z, (uint32_t)raw.w);
                 lds_char* dst = lds + AREA + blk * DD::STAGE + which * DD::REGION * 16;
                 *reinterpret_cast<__attribute__((address_space(3))) h8*>(dst + slot_of(2 * ch, key) * 16) = lo;
                 *reinterpret_cast<__attribute__((address_space(3))) h8*>(dst + slot_of(2 * ch + 1, key) * 16) = hi;
@@ -357,7 +358,7 @@ void prefill_dma_kernel(PrefillParams p) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
         m_run[rb] = kMaxSeed;
-        thr[rb] = I8 ? kMaxSeed + kLazy : (kMaxSeed + kLazy) * inv_scale;
+        thr[rb] = SCALED ? kMaxSeed + kLazy : (kMaxSeed + kLazy) * inv_scale;
     }
 
     // LDS byte offsets of this lane's fragment reads: one base each plus
@@ -375,7 +376,7 @@ void prefill_dma_kernel(PrefillParams p) {
 
     auto compute = [&](int kb, auto masked_tag) {
         constexpr bool MASKED = decltype(masked_tag)::value;
-        lds_char* sb = I8 ? lds + AREA + (kb & 1) * DD::STAGE : lds + (kb % kStages) * DD::STAGE;
+        lds_char* sb = BYTES ? lds + AREA + (kb & 1) * DD::STAGE : lds + (kb % kStages) * DD::STAGE;
         const int key0 = kb * kKBlk;
         h8 ka[2][NC32 > 0 ? NC32 : 1];
         h8 kr[2];
@@ -420,7 +421,7 @@ void prefill_dma_kernel(PrefillParams p) {
         // int8 pages: S times the key's scale (log2 units).
         auto s_group = [&](int rb0, float (&sc)[SG][2][4], float (&mx)[SG]) {
             float ks[2][4];  // int8: K scales times log2(e) / sqrt(D)
-            if constexpr (I8) {
+            if constexpr (SCALED) {
                 scales(0, ks);
 #pragma unroll
                 for (int kt = 0; kt < 2; ++kt)
@@ -439,7 +440,7 @@ void prefill_dma_kernel(PrefillParams p) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         float x = acc[r];
-                        if constexpr (I8) x *= ks[kt][r];
+                        if constexpr (SCALED) x *= ks[kt][r];
                         if constexpr (MASKED) {
                             const int key = key0 + 16 * kt + 4 * g + r;
                             const int lim = min(prefix + t0 + 16 * rb + c, kv_end - 1);
@@ -466,7 +467,7 @@ void prefill_dma_kernel(PrefillParams p) {
                     const float mr = max_over_groups(mx[i]);
                     const bool grow = mr > thr[rb];  // uniform per row
                     float alpha;
-                    if constexpr (I8) {
+                    if constexpr (SCALED) {
                         const float m_new = grow ? mr : m_run[rb];
                         alpha = fast_exp2(m_run[rb] - m_new);
                         m_run[rb] = m_new;
@@ -490,14 +491,14 @@ void prefill_dma_kernel(PrefillParams p) {
         };
         auto p_group = [&](int rb0, const float (&sc)[SG][2][4], h8 (&pa)[SG]) {
             float vs[2][4];  // int8: V scales
-            if constexpr (I8) scales(1, vs);
+            if constexpr (SCALED) scales(1, vs);
 #pragma unroll
             for (int i = 0; i < SG; ++i)
 #pragma unroll
                 for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        if constexpr (I8) {
+                        if constexpr (SCALED) {
                             // P (fp32) into the row sum; P times the V scale,
                             // rounded once, weights the int8 V values.
                             const float pr = fast_exp2(sc[i][kt][r] - m_run[rb0 + i]);
@@ -513,7 +514,7 @@ void prefill_dma_kernel(PrefillParams p) {
             for (int i = 0; i < SG; ++i) {
 #pragma unroll
                 for (int t = 0; t < NT; ++t) o[rb0 + i][t] = mfma32(pa[i], vb[t], o[rb0 + i][t]);
-                if constexpr (!I8) {  // row sums of exactly the fp16 P that weights V
+                if constexpr (!SCALED) {  // row sums of exactly the fp16 P that weights V
 #pragma unroll
                     for (int e = 0; e < 8; e += 2)
                         lsum[rb0 + i] =
@@ -534,7 +535,7 @@ void prefill_dma_kernel(PrefillParams p) {
             const bool more = j + 1 < RB / SG;
             const int nx = (j + 1) & 1;
             p_group(j * SG, sc[j & 1], pa);
-            if constexpr (!I8) {
+            if constexpr (!SCALED) {
                 if (more) s_group((j + 1) * SG, sc[nx], mx[nx]);
                 pv_group(j * SG, pa);
             } else {
@@ -551,7 +552,7 @@ void prefill_dma_kernel(PrefillParams p) {
     // vmcnt arithmetic below stays exact, and an odd tail block is paired
     // with a fully masked one.
     static_assert(kStages >= 4 && kStages % 2 == 0, "ring holds whole pairs");
-    if constexpr (I8) {
+    if constexpr (BYTES) {
 #pragma unroll
         for (int s = 0; s < kStages - 2; ++s) issue8(s);
     } else {
@@ -561,7 +562,7 @@ void prefill_dma_kernel(PrefillParams p) {
     const int free_end = any_bad ? 0 : (min(nfree, nblk) & ~1);
     auto step = [&](int kb) {
         constexpr int kAhead = kStages - 4;  // blocks allowed in flight at the wait
-        if constexpr (I8) {
+        if constexpr (BYTES) {
             if (my_inst8 == PERW8) wait_vmcnt<kAhead * PERW8>();
             else wait_vmcnt<kAhead * (PERW8 - 1)>();
             __syncthreads();  // blocks kb, kb + 1 landed; the fp16 area is free again
@@ -631,7 +632,9 @@ size_t prefill_lds_bytes(int kv_dtype, int head_dim, int max_blocks) {
     auto ring = [&](auto d) -> size_t {
         constexpr int D = decltype(d)::value;
         if (kv_dtype == VCPP_KV_I8)
-            return (size_t)I8Dims<D>::STAGES * I8Dims<D>::STAGE + 2 * (size_t)DmaDims<D>::STAGE;
+            return (size_t)ByteDims<D, true>::STAGES * ByteDims<D, true>::STAGE + 2 * (size_t)DmaDims<D>::STAGE;
+        if (kv_dtype == VCPP_KV_FP8)
+            return (size_t)ByteDims<D, false>::STAGES * ByteDims<D, false>::STAGE + 2 * (size_t)DmaDims<D>::STAGE;
         return (size_t)DmaDims<D>::STAGES * DmaDims<D>::STAGE;
     };
     size_t r = 0;
@@ -658,6 +661,8 @@ hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream) {
     }
     if (p.kv_dtype == VCPP_KV_F16) {
         VCPP_PF_D(VCPP_KV_F16)
+    } else if (p.kv_dtype == VCPP_KV_FP8) {
+        VCPP_PF_D(VCPP_KV_FP8)
     } else {
         VCPP_PF_D(VCPP_KV_I8)
     }

@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdint>
 #include <cstring>
 #include <stdexcept>
@@ -34,6 +35,16 @@ inline bool is_device(const void* p) {
 
 // The reference's fp16 -> fp32 decoder (src/kv_cache_manager.cpp:120-143):
 // exact for zeros, subnormals and normals; exponent 31 gives +/-inf.
+// FP8 E4M3 as the reference KV pool stores it (src/quantization.cpp:25-48):
+// bias 7, exponent 15 = inf (mantissa 6) or NaN.
+inline float fp8_decode(uint8_t b) {
+    const int sign = (b >> 7) & 1, e = (b >> 3) & 0xF, m = b & 7;
+    if (e == 0xF) return m == 6 ? (sign ? -INFINITY : INFINITY) : NAN;
+    const float v = e == 0 ? (float)m / 8.0f * std::ldexp(1.0f, -6)
+                           : (1.0f + (float)m / 8.0f) * std::ldexp(1.0f, e - 7);
+    return sign ? -v : v;
+}
+
 inline float f16_decode(uint16_t h) {
     const uint32_t s = (h >> 15) & 1u, e = (h >> 10) & 0x1Fu;
     uint32_t f = h & 0x3FFu;

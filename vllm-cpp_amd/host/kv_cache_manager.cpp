@@ -26,6 +26,9 @@ void decode_rows(const uint8_t* raw, const uint16_t* scales, float* out, int32_t
             for (int32_t i = 0; i < n; ++i) out[i] = vcpp_host::f16_decode(h[i]);
             break;
         }
+        case KVDtype::FP8_E4M3:
+            for (int32_t i = 0; i < n; ++i) out[i] = vcpp_host::fp8_decode(raw[i]);
+            break;
         case KVDtype::INT8: {
             const int8_t* q = reinterpret_cast<const int8_t*>(raw);
             const int32_t hkv = kv_dim / head_dim;
@@ -52,8 +55,6 @@ BlockPool::BlockPool(int32_t num_blocks, int32_t num_layers, int32_t kv_dim, KVD
                      int32_t head_dim)
     : kv_dim_(kv_dim), num_layers_(num_layers), kv_dtype_(kv_dtype),
       head_dim_(head_dim > 0 ? head_dim : kv_dim) {
-    if (kv_dtype == KVDtype::FP8_E4M3)
-        throw std::invalid_argument("BlockPool: FP8_E4M3 pages are not supported on the GPU");
     if (num_blocks < 0 || num_layers <= 0 || kv_dim <= 0 || kv_dim % head_dim_ != 0)
         throw std::invalid_argument("BlockPool: bad shape");
     if (kv_dtype == KVDtype::INT8 && head_dim <= 0)
@@ -262,7 +263,12 @@ const KVsBlock& BlockPool::get_block(int32_t block_id) const { return blocks_[bl
 
 vcpp_kv_pages BlockPool::pages(int32_t layer) const {
     vcpp_kv_pages p{};
-    p.dtype = kv_dtype_ == KVDtype::FP32 ? VCPP_KV_F32 : kv_dtype_ == KVDtype::FP16 ? VCPP_KV_F16 : VCPP_KV_I8;
+    switch (kv_dtype_) {
+        case KVDtype::FP32: p.dtype = VCPP_KV_F32; break;
+        case KVDtype::FP16: p.dtype = VCPP_KV_F16; break;
+        case KVDtype::FP8_E4M3: p.dtype = VCPP_KV_FP8; break;
+        default: p.dtype = VCPP_KV_I8; break;
+    }
     p.block_size = BLOCK_SIZE;
     p.num_kv_heads = kv_dim_ / head_dim_;
     p.head_dim = head_dim_;

@@ -21,6 +21,7 @@ VCPP_E_HIP = -4
 KV_F32 = 0
 KV_F16 = 1
 KV_I8 = 2
+KV_FP8 = 3
 
 # Every symbol include/vcpp_attention.h declares.
 EXPORTS = [
