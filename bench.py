@@ -12,6 +12,10 @@ input resident in HBM.  Algorithmic bytes = K and V pages of every context
 token (2 * Hkv * D * 2 B per token) + q and out (fp32) + block-table entries.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20]
+
+Every leg warms up with at least its warmup count and at least 50 ms of GPU
+work before its timed steps: a fresh MI355X raises its clocks over the first
+~30 ms of load, and timing that ramp would under-report.
 """
 import argparse
 import ctypes
@@ -134,8 +138,7 @@ def run_prefill_steps(pyvcpp, pw, steps):
 
 def bench_prefill(torch, pyvcpp, args):
     pw = prefill_workload(torch, args.seed + 7)
-    run_prefill_steps(pyvcpp, pw, 3)
-    torch.cuda.synchronize()
+    settle(torch, lambda: run_prefill_steps(pyvcpp, pw, 1), 3)
     t0 = time.perf_counter()
     run_prefill_steps(pyvcpp, pw, args.prefill_steps)
     torch.cuda.synchronize()
@@ -169,10 +172,22 @@ def bench_prefill(torch, pyvcpp, args):
 # ---------------------------------------------------------------------------
 # config 4: long-context decode; config 5: int8 mixed decode + prefill step
 
-def timed(torch, fn, steps, warmup=3):
-    for _ in range(warmup):
+def settle(torch, fn, warmup=3, seconds=0.05):
+    """Untimed warmup: at least `warmup` calls and at least `seconds` of GPU
+    work, so the timed steps run at the clocks the GPU holds under load (they
+    ramp up over the first ~30 ms of work on a fresh box)."""
+    t0 = time.perf_counter()
+    i = 0
+    while i < warmup or time.perf_counter() - t0 < seconds:
         fn()
+        i += 1
+        if i % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
+
+
+def timed(torch, fn, steps, warmup=3):
+    settle(torch, fn, warmup)
     t0 = time.perf_counter()
     for _ in range(steps):
         fn()
@@ -437,7 +452,7 @@ def main():
     ws = torch.zeros(max(need, 1), dtype=torch.uint8, device="cuda:0")
 
     run_decode_steps(torch, pyvcpp, w, args.warmup, ws, args.partition)
-    torch.cuda.synchronize()
+    settle(torch, lambda: run_decode_steps(torch, pyvcpp, w, 1, ws, args.partition), 0)
     t0 = time.perf_counter()
     run_decode_steps(torch, pyvcpp, w, args.steps, ws, args.partition)
     torch.cuda.synchronize()

@@ -614,10 +614,14 @@ hipError_t launch_dma(const PrefillParams& p, hipStream_t stream) {
     dim3 grid((p.max_chunk_len + QT - 1) / QT, p.num_chunks,
               p.num_kv_heads * p.head_groups);
     const size_t lds = prefill_lds_bytes(KV, D, p.max_blocks);
-    if (lds > 65536) {
+    // Raise the kernel's dynamic LDS limit only when a launch needs more than
+    // it was last set to (the attribute call is a host round trip).
+    static size_t attr_lds = 65536;  // one device per process
+    if (lds > attr_lds) {
         const hipError_t e = hipFuncSetAttribute((const void*)prefill_dma_kernel<KV, D>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
+        attr_lds = lds;
     }
     hipLaunchKernelGGL((prefill_dma_kernel<KV, D>), grid, dim3(256), lds, stream, p);
     return hipGetLastError();
