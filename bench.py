@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the config 4 (long context) and config 5 (int8 mixed) legs")
     ap.add_argument("--config-steps", type=int, default=20)
-    ap.add_argument("--only", choices=["decode", "prefill", "config4", "config5", "qkprep"],
+    ap.add_argument("--only", choices=["decode", "prefill", "config4", "config5", "qkprep", "fp8"],
                     help="run one leg only and print its JSON (for profiling)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the prefill leg (for profiling its kernel)")
@@ -371,6 +371,53 @@ def read_traffic(name):
     return None
 
 
+def bench_fp8(torch, pyvcpp, args):
+    """Config 2's sequences and tables on FP8 E4M3 pages (the reference's
+    KV_FP8 format, written on the device by vcpp_write_kv from the same N(0,1)
+    values): 1,280 bytes per context token."""
+    w = decode_workload(torch, args.seed, pools=3)
+    dev = torch.device("cuda:0")
+    sets = []
+    nrows = w["nb"] * BS
+    slots = torch.arange(nrows, dtype=torch.int64, device=dev)
+    for k16, v16, tables in w["sets"]:
+        k8 = torch.empty((w["nb"], BS, HKV, D), dtype=torch.uint8, device=dev)
+        v8 = torch.empty_like(k8)
+        pg = pyvcpp.kv_pages(pyvcpp.KV_FP8, k8, v8, BS, HKV, D, w["nb"], BS * HKV * D)
+        pyvcpp.write_kv(pg, k16.float().view(nrows, HKV, D), v16.float().view(nrows, HKV, D), slots)
+        sets.append((pg, k8, v8, tables))
+    torch.cuda.synchronize()
+    need = pyvcpp.decode_workspace_size(sets[0][0], 64, H, w["max_ctx"], 0)
+    ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=dev)
+    it = [0]
+
+    def step():
+        pg, _, _, tb = sets[it[0] % 3]
+        it[0] += 1
+        pyvcpp.paged_decode(pg, w["q"], w["out"], tb, w["ctx_dev"], w["max_ctx"], H, workspace=ws)
+    steps = max(args.config_steps, 50)
+    dt = timed(torch, step, steps)
+    pyvcpp.profile_enable(True)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms, n = pyvcpp.profile_read(pyvcpp.KERNEL_DECODE)
+    mms, mn = pyvcpp.profile_read(pyvcpp.KERNEL_MERGE)
+    pyvcpp.profile_enable(False)
+    k_s = ms / max(n, 1) / 1e3
+    nbytes = (w["total_tokens"] * 2 * HKV * D + 64 * H * D * 8 + sum(w["nblk"]) * 4)
+    return {
+        "metric": "fp8-page decode HBM TB/s", "value": round(nbytes / dt / 1e12, 4), "unit": "TB/s",
+        "ms_per_step": round(dt * 1e3, 4), "steps": steps,
+        "config": {"workload": "config 2 sequences (64, ctx U[128,4096]) on FP8 E4M3 pages, 64 q / 8 kv "
+                               "heads, head_dim 80", "bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(nbytes / k_s / 1e9, 1), "peak": HBM_PEAK_TBS * 1e3,
+                     "unit": "GB/s", "frac": round(nbytes / k_s / 1e12 / HBM_PEAK_TBS, 4),
+                     "kernel": "decode_page_kernel<fp8,80>", "kernel_avg_us": round(k_s * 1e6, 2),
+                     "merge_avg_us": round(mms / max(mn, 1) * 1e3, 2)},
+    }
+
+
 def bench_qkprep(torch, pyvcpp, args):
     """Fused q/k norm + RoPE (vcpp_qk_norm_rope) over config 3's 16384 prefill
     tokens: q [16384][64][80], k [16384][8][80] fp32 at positions 1024..3071,
@@ -444,6 +491,9 @@ def main():
     if args.only == "qkprep":
         print(json.dumps(bench_qkprep(torch, pyvcpp, args)))
         return
+    if args.only == "fp8":
+        print(json.dumps(bench_fp8(torch, pyvcpp, args)))
+        return
 
     w = decode_workload(torch, args.seed)
     pages0 = pyvcpp.kv_pages(pyvcpp.KV_F16, w["sets"][0][0], w["sets"][0][1], BS, HKV, D, w["nb"],
@@ -504,6 +554,7 @@ def main():
         result["config4"] = bench_config4(torch, pyvcpp, args)
         result["config5"] = bench_config5(torch, pyvcpp, args)
         result["qk_prep"] = bench_qkprep(torch, pyvcpp, args)
+        result["fp8_decode"] = bench_fp8(torch, pyvcpp, args)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(torch, w, args.cpu_seconds)
     else:
