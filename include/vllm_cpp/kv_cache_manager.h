@@ -17,6 +17,7 @@
 #pragma once
 
 #include <cstdint>
+#include <memory>
 #include <mutex>
 #include <vector>
 
@@ -75,6 +76,14 @@ public:
 
     void copy_to(int32_t dst, int32_t src);  // all layers (and scales) of src -> dst
 
+    // Bytes of one block's pages in host memory: K and V of every layer, then
+    // the INT8 scales.  copy_out / copy_in move them between a block and host
+    // memory on the pool's stream (asynchronous; the host buffer must be
+    // pinned and live until the stream has passed the copy).
+    size_t block_host_bytes() const;
+    void copy_out(int32_t block_id, void* host) const;
+    void copy_in(int32_t block_id, const void* host);
+
     int32_t free_count() const;
     int32_t used_count() const;
     void reset();  // every block free, all data zero
@@ -117,6 +126,23 @@ private:
     mutable std::mutex mtx_;
 };
 
+// Pages of some blocks kept in pinned host memory by KVCacheManager::swap_out.
+class KVSwap {
+public:
+    ~KVSwap();  // waits for the stream that filled it, then frees the memory
+    KVSwap(const KVSwap&) = delete;
+    KVSwap& operator=(const KVSwap&) = delete;
+    int32_t num_blocks() const { return num_blocks_; }
+
+private:
+    friend class KVCacheManager;
+    KVSwap() = default;
+    void* host_ = nullptr;
+    size_t block_bytes_ = 0;
+    int32_t num_blocks_ = 0;
+    void* stream_ = nullptr;
+};
+
 class KVCacheManager {
 public:
     KVCacheManager(int32_t num_layers, int32_t kv_dim, int32_t num_blocks,
@@ -126,6 +152,17 @@ public:
     bool alloc_blocks(int32_t num_blocks, std::vector<int32_t>& out);
     void free_blocks(const std::vector<int32_t>& blocks_to_free);
     void copy_blocks(const std::vector<int32_t>& src, const std::vector<int32_t>& dst);
+
+    // Preemption that keeps the data (no counterpart in the reference, whose
+    // Scheduler keeps only block ids across a preemption and restores by
+    // copy_blocks from blocks it has already freed, i.e. zeroed:
+    // src/scheduler.cpp:87-153).  swap_out copies the blocks' pages (every
+    // layer, K, V and INT8 scales) to pinned host memory, queued on the pool's
+    // stream ahead of the free that may follow; swap_in copies them into the
+    // same number of (newly allocated) blocks.  Invalid ids are skipped;
+    // swap_in returns false when the counts differ.
+    std::unique_ptr<KVSwap> swap_out(const std::vector<int32_t>& blocks);
+    bool swap_in(const KVSwap& swap, const std::vector<int32_t>& blocks);
 
     BlockPool& block_pool() { return pool_; }
     const BlockPool& block_pool() const { return pool_; }

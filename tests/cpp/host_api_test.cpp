@@ -78,6 +78,8 @@ struct HostLayer {
                 std::memcpy(dst.data() + off * 4, src, sizeof(float) * hkv * d);
             } else if (dtype == KVDtype::FP16) {
                 orc_f16_encode_trunc_n(src, reinterpret_cast<uint16_t*>(dst.data()) + off, (int64_t)hkv * d);
+            } else if (dtype == KVDtype::FP8_E4M3) {
+                orc_fp8_encode_n(src, dst.data() + off, (int64_t)hkv * d);
             } else {
                 std::vector<uint16_t>& sc = which ? vs : ks;
                 for (int32_t h = 0; h < hkv; ++h) {
@@ -90,7 +92,10 @@ struct HostLayer {
     }
     orc_pool pool(int32_t layer) const {
         orc_pool p{};
-        p.kind = dtype == KVDtype::FP32 ? ORC_F32 : dtype == KVDtype::FP16 ? ORC_F16 : ORC_I8;
+        p.kind = dtype == KVDtype::FP32       ? ORC_F32
+                 : dtype == KVDtype::FP16     ? ORC_F16
+                 : dtype == KVDtype::FP8_E4M3 ? ORC_FP8
+                                              : ORC_I8;
         const int64_t esz = kv_elem_size(dtype);
         p.k = k.data() + (int64_t)layer * 16 * hkv * d * esz;
         p.v = v.data() + (int64_t)layer * 16 * hkv * d * esz;
@@ -160,6 +165,7 @@ void test_write_read(KVDtype dt) {
         for (int32_t j = 0; j < kv; ++j) {
             if (dt == KVDtype::FP32) want[j] = k[i * kv + j];
             else if (dt == KVDtype::FP16) want[j] = orc_f16_decode(orc_f16_encode_trunc(k[i * kv + j]));
+            else if (dt == KVDtype::FP8_E4M3) want[j] = orc_fp8_decode(orc_fp8_encode(k[i * kv + j]));
             else {
                 const int32_t h = j / D;
                 const int8_t q = reinterpret_cast<const int8_t*>(op.k)[blocks[i % 3] * op.block_stride + pos[i] * kv + j];
@@ -181,6 +187,39 @@ void test_write_read(KVDtype dt) {
     CHECK(zero, "freed block zeroed");
     static const char* names[] = {"FP32", "FP16", "FP8", "INT8"};
     std::printf("ok   write_kv / read_kv / copy_blocks / free on %-12s (bit-exact)\n", names[(int)dt]);
+}
+
+// Preemption that keeps the data: swap_out before free, swap_in into the
+// blocks allocated on restore (which the free zeroed or another request used).
+void test_swap(KVDtype dt) {
+    const int32_t L = 3, H = 4, D = 80, kv = H * D;
+    KVCacheManager m(L, kv, 6, dt, D);
+    std::vector<int32_t> blocks;
+    CHECK(m.alloc_blocks(3, blocks), "alloc_blocks");
+    auto k = normal(31, kv * 6, 2.0), v = normal(32, kv * 6, 2.0);
+    for (int i = 0; i < 6; ++i)
+        m.write_kv(blocks[i % 3], i % L, 2 * i, k.data() + i * kv, v.data() + i * kv, kv);
+    std::vector<float> before(6 * kv), vb(6 * kv);
+    for (int i = 0; i < 6; ++i)
+        m.read_kv(blocks[i % 3], i % L, 2 * i, before.data() + i * kv, vb.data() + i * kv, kv);
+    auto sw = m.swap_out(blocks);
+    m.free_blocks(blocks);  // zeroes them (after the copy, same stream)
+    std::vector<int32_t> other, again;
+    CHECK(m.alloc_blocks(2, other), "alloc other");  // reuses freed ids
+    auto junk = normal(33, kv, 5.0);
+    for (int32_t b : other) m.write_kv(b, 0, 0, junk.data(), junk.data(), kv);
+    CHECK(m.alloc_blocks(3, again), "alloc restore");
+    CHECK(m.swap_in(*sw, again), "swap_in");
+    CHECK(!m.swap_in(*sw, other), "swap_in rejects a different block count");
+    std::vector<float> after(kv), va(kv);
+    for (int i = 0; i < 6; ++i) {
+        m.read_kv(again[i % 3], i % L, 2 * i, after.data(), va.data(), kv);
+        CHECK(std::memcmp(after.data(), before.data() + i * kv, sizeof(float) * kv) == 0 &&
+                  std::memcmp(va.data(), vb.data() + i * kv, sizeof(float) * kv) == 0,
+              "swapped-in row %d", i);
+    }
+    static const char* names[] = {"FP32", "FP16", "FP8", "INT8"};
+    std::printf("ok   swap_out / free / swap_in on %-12s (bit-exact)\n", names[(int)dt]);
 }
 
 void test_attention(KVDtype dt) {
@@ -260,6 +299,7 @@ void test_attention(KVDtype dt) {
             const int64_t e = tables[1][p / 16] * op.block_stride + (int64_t)(p % 16) * kv + j;
             if (dt == KVDtype::FP32) want_k = reinterpret_cast<const float*>(op.k)[e];
             else if (dt == KVDtype::FP16) want_k = orc_f16_decode(reinterpret_cast<const uint16_t*>(op.k)[e]);
+            else if (dt == KVDtype::FP8_E4M3) want_k = orc_fp8_decode(reinterpret_cast<const uint8_t*>(op.k)[e]);
             else want_k = (float)reinterpret_cast<const int8_t*>(op.k)[e] *
                           orc_f16_decode(op.k_scale[tables[1][p / 16] * op.scale_block_stride + (j / D) * 16 + p % 16]);
             CHECK(rk[(size_t)p * kv + j] == want_k, "read_kv_prefill pos %d dim %d", p, j);
@@ -279,9 +319,12 @@ int main() {
         return 2;
     }
     test_bookkeeping();
-    for (KVDtype dt : {KVDtype::FP32, KVDtype::FP16, KVDtype::INT8}) test_write_read(dt);
-    for (KVDtype dt : {KVDtype::FP32, KVDtype::FP16, KVDtype::INT8}) {
-        std::printf("---- attention on %s pages\n", dt == KVDtype::FP32 ? "FP32" : dt == KVDtype::FP16 ? "FP16" : "INT8");
+    const KVDtype all[] = {KVDtype::FP32, KVDtype::FP16, KVDtype::FP8_E4M3, KVDtype::INT8};
+    static const char* names[] = {"FP32", "FP16", "FP8", "INT8"};
+    for (KVDtype dt : all) test_write_read(dt);
+    for (KVDtype dt : all) test_swap(dt);
+    for (KVDtype dt : all) {
+        std::printf("---- attention on %s pages\n", names[(int)dt]);
         test_attention(dt);
     }
     std::printf("ALL PASSED (%d checks)\n", g_checks);

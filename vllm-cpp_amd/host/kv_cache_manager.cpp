@@ -282,6 +282,78 @@ vcpp_kv_pages BlockPool::pages(int32_t layer) const {
     return p;
 }
 
+size_t BlockPool::block_host_bytes() const {
+    size_t n = 2 * (size_t)block_bytes_;
+    if (k_scale_) n += 2 * sizeof(uint16_t) * (size_t)(scale_layer_ * num_layers_);
+    return n;
+}
+
+void BlockPool::copy_out(int32_t block_id, void* host) const {
+    if (block_id < 0 || block_id >= (int32_t)blocks_.size()) return;
+    hipStream_t s = static_cast<hipStream_t>(stream_);
+    uint8_t* h = static_cast<uint8_t*>(host);
+    check(hipMemcpyAsync(h, k_ + (int64_t)block_id * block_bytes_, block_bytes_, hipMemcpyDeviceToHost, s),
+          "copy_out K");
+    check(hipMemcpyAsync(h + block_bytes_, v_ + (int64_t)block_id * block_bytes_, block_bytes_,
+                         hipMemcpyDeviceToHost, s), "copy_out V");
+    if (k_scale_) {
+        const int64_t n = scale_layer_ * num_layers_;
+        uint8_t* hs = h + 2 * block_bytes_;
+        check(hipMemcpyAsync(hs, k_scale_ + block_id * n, sizeof(uint16_t) * n, hipMemcpyDeviceToHost, s),
+              "copy_out K scales");
+        check(hipMemcpyAsync(hs + sizeof(uint16_t) * n, v_scale_ + block_id * n, sizeof(uint16_t) * n,
+                             hipMemcpyDeviceToHost, s), "copy_out V scales");
+    }
+}
+
+void BlockPool::copy_in(int32_t block_id, const void* host) {
+    if (block_id < 0 || block_id >= (int32_t)blocks_.size()) return;
+    hipStream_t s = static_cast<hipStream_t>(stream_);
+    const uint8_t* h = static_cast<const uint8_t*>(host);
+    check(hipMemcpyAsync(k_ + (int64_t)block_id * block_bytes_, h, block_bytes_, hipMemcpyHostToDevice, s),
+          "copy_in K");
+    check(hipMemcpyAsync(v_ + (int64_t)block_id * block_bytes_, h + block_bytes_, block_bytes_,
+                         hipMemcpyHostToDevice, s), "copy_in V");
+    if (k_scale_) {
+        const int64_t n = scale_layer_ * num_layers_;
+        const uint8_t* hs = h + 2 * block_bytes_;
+        check(hipMemcpyAsync(k_scale_ + block_id * n, hs, sizeof(uint16_t) * n, hipMemcpyHostToDevice, s),
+              "copy_in K scales");
+        check(hipMemcpyAsync(v_scale_ + block_id * n, hs + sizeof(uint16_t) * n, sizeof(uint16_t) * n,
+                             hipMemcpyHostToDevice, s), "copy_in V scales");
+    }
+}
+
+// ---- KVSwap / KVCacheManager -------------------------------------------------
+
+KVSwap::~KVSwap() {
+    if (host_) {
+        (void)hipStreamSynchronize(static_cast<hipStream_t>(stream_));
+        (void)hipHostFree(host_);
+    }
+}
+
+std::unique_ptr<KVSwap> KVCacheManager::swap_out(const std::vector<int32_t>& blocks) {
+    std::unique_ptr<KVSwap> sw(new KVSwap());
+    sw->block_bytes_ = pool_.block_host_bytes();
+    sw->num_blocks_ = (int32_t)blocks.size();
+    sw->stream_ = pool_.stream();
+    if (!blocks.empty())
+        check(hipHostMalloc(&sw->host_, sw->block_bytes_ * blocks.size(), hipHostMallocDefault),
+              "swap_out host memory");
+    for (size_t i = 0; i < blocks.size(); ++i)
+        pool_.copy_out(blocks[i], static_cast<uint8_t*>(sw->host_) + i * sw->block_bytes_);
+    return sw;
+}
+
+bool KVCacheManager::swap_in(const KVSwap& swap, const std::vector<int32_t>& blocks) {
+    if ((int32_t)blocks.size() != swap.num_blocks_ || swap.block_bytes_ != pool_.block_host_bytes())
+        return false;
+    for (size_t i = 0; i < blocks.size(); ++i)
+        pool_.copy_in(blocks[i], static_cast<const uint8_t*>(swap.host_) + i * swap.block_bytes_);
+    return true;
+}
+
 // ---- KVCacheManager ---------------------------------------------------------
 
 KVCacheManager::KVCacheManager(int32_t num_layers, int32_t kv_dim, int32_t num_blocks,
