@@ -50,7 +50,8 @@ def parse():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the config 4 (long context) and config 5 (int8 mixed) legs")
     ap.add_argument("--config-steps", type=int, default=20)
-    ap.add_argument("--only", choices=["decode", "prefill", "config4", "config5", "qkprep", "fp8"],
+    ap.add_argument("--only", choices=["decode", "prefill", "config4", "config5", "qkprep", "fp8",
+                                       "kvwrite"],
                     help="run one leg only and print its JSON (for profiling)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the prefill leg (for profiling its kernel)")
@@ -418,6 +419,46 @@ def bench_fp8(torch, pyvcpp, args):
     }
 
 
+def bench_kvwrite(torch, pyvcpp, args):
+    """vcpp_write_kv of config 3's 16384 prefill tokens (8 chunks x 2048 on
+    1024-token prefixes): K and V fp32 [16384][8][80] into pages, fp16 (the
+    reference's truncating encoder), int8 + scale and FP8.  HBM-bound: every
+    fp32 value read once, its encoding written once."""
+    dev = torch.device("cuda:0")
+    T, chunks, new, prefix = 8 * 2048, 8, 2048, 1024
+    nblk = (prefix + new) // BS
+    nb = chunks * nblk
+    g = torch.Generator(device=dev).manual_seed(args.seed + 70)
+    k = torch.randn((T, HKV, D), generator=g, device=dev)
+    v = torch.randn((T, HKV, D), generator=g, device=dev)
+    perm = torch.randperm(nb, device="cpu").to(torch.int64).view(chunks, nblk)
+    pos = torch.arange(new, dtype=torch.int64) + prefix
+    slots = torch.cat([perm[c, pos // BS] * BS + pos % BS for c in range(chunks)]).to(dev)
+    out = {}
+    for name, dt, es in (("fp16", pyvcpp.KV_F16, 2), ("int8", pyvcpp.KV_I8, 1), ("fp8", pyvcpp.KV_FP8, 1)):
+        tdt = torch.float16 if es == 2 else torch.uint8
+        kp = torch.zeros((nb, BS, HKV, D), dtype=tdt, device=dev)
+        vp = torch.zeros_like(kp)
+        ks = vs = None
+        if dt == pyvcpp.KV_I8:
+            ks = torch.zeros((nb, HKV, BS), dtype=torch.float16, device=dev)
+            vs = torch.zeros_like(ks)
+        pg = pyvcpp.kv_pages(dt, kp, vp, BS, HKV, D, nb, BS * HKV * D, ks, vs, HKV * BS)
+        nbytes = 2 * T * HKV * D * (4 + es) + T * 8 + (2 * T * HKV * 2 if dt == pyvcpp.KV_I8 else 0)
+        steps = max(args.config_steps, 20)
+        dt_s = timed(torch, lambda: pyvcpp.write_kv(pg, k, v, slots), steps)
+        out[name] = {"us": round(dt_s * 1e6, 2), "TB/s": round(nbytes / dt_s / 1e12, 3), "bytes": nbytes}
+    f = out["fp16"]
+    return {
+        "metric": "KV page write HBM TB/s", "value": f["TB/s"], "unit": "TB/s",
+        "config": {"workload": "config 3 chunk tokens: 16384 x 8 kv heads x 80, K and V fp32 -> pages "
+                               "(value: fp16, the reference's truncating encoder)"},
+        "roofline": {"bound": "hbm", "achieved": round(f["TB/s"] * 1e3, 1), "peak": HBM_PEAK_TBS * 1e3,
+                     "unit": "GB/s", "frac": round(f["TB/s"] / HBM_PEAK_TBS, 4), "kernel": "kv_write_vec_kernel"},
+        "variants": out,
+    }
+
+
 def bench_qkprep(torch, pyvcpp, args):
     """Fused q/k norm + RoPE (vcpp_qk_norm_rope) over config 3's 16384 prefill
     tokens: q [16384][64][80], k [16384][8][80] fp32 at positions 1024..3071,
@@ -494,6 +535,9 @@ def main():
     if args.only == "fp8":
         print(json.dumps(bench_fp8(torch, pyvcpp, args)))
         return
+    if args.only == "kvwrite":
+        print(json.dumps(bench_kvwrite(torch, pyvcpp, args)))
+        return
 
     w = decode_workload(torch, args.seed)
     pages0 = pyvcpp.kv_pages(pyvcpp.KV_F16, w["sets"][0][0], w["sets"][0][1], BS, HKV, D, w["nb"],
@@ -555,6 +599,7 @@ def main():
         result["config5"] = bench_config5(torch, pyvcpp, args)
         result["qk_prep"] = bench_qkprep(torch, pyvcpp, args)
         result["fp8_decode"] = bench_fp8(torch, pyvcpp, args)
+        result["kv_write"] = bench_kvwrite(torch, pyvcpp, args)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(torch, w, args.cpu_seconds)
     else:

@@ -151,3 +151,40 @@ def test_write_then_prefill(cuda, kind):
     want = O.prefill(host, q16.astype(np.float32), tables, q_start, prefix, H)
     got = gpu_prefill(dp, q16.view(np.uint16), tables, q_start, prefix, H)
     assert_close(got, want, 2e-3, 1e-2, what="write then prefill kind=%d" % kind)
+
+
+@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8, O.ORC_FP8])
+def test_write_kv_generic_path(cuda, kind):
+    """head_dim 10 (not a multiple of 4): the one-wave-per-row writer."""
+    nb, bs, hkv, d, n = 6, 16, 3, 10, 50
+    x = O.normal(91, (n, hkv, d), 0.0, 4.0)
+    y = O.normal(92, (n, hkv, d), 0.0, 4.0)
+    slots = O.permutation(93, nb * bs)[:n].astype(np.int64)
+    shape = (nb, bs, hkv, d)
+    if kind == O.ORC_F16:
+        host = O.Pool(kind, np.zeros(shape, np.uint16), np.zeros(shape, np.uint16))
+    elif kind == O.ORC_FP8:
+        host = O.Pool(kind, np.zeros(shape, np.uint8), np.zeros(shape, np.uint8))
+    else:
+        host = O.Pool(kind, np.zeros(shape, np.int8), np.zeros(shape, np.int8),
+                      np.zeros((nb, hkv, bs), np.uint16), np.zeros((nb, hkv, bs), np.uint16))
+    dp = DevPool(host)
+    pyvcpp.write_kv(dp.pages, dev(x), dev(y), dev(slots))
+    torch.cuda.synchronize()
+    gk, gv, gks, gvs = readback(dp, kind)
+    for t, s in enumerate(slots):
+        b, p = divmod(int(s), bs)
+        for src, dst, sdst in ((x[t], host.k, host.k_scale), (y[t], host.v, host.v_scale)):
+            if kind == O.ORC_F16:
+                dst[b, p] = O.f16_trunc(src)
+            elif kind == O.ORC_FP8:
+                dst[b, p] = O.fp8_encode(src)
+            else:
+                q, sc = O.quant_i8(src)
+                dst[b, p] = q
+                sdst[b, :, p] = sc
+    np.testing.assert_array_equal(gk, host.k)
+    np.testing.assert_array_equal(gv, host.v)
+    if kind == O.ORC_I8:
+        np.testing.assert_array_equal(gks, host.k_scale)
+        np.testing.assert_array_equal(gvs, host.v_scale)

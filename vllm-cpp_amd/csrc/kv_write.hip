@@ -3,7 +3,9 @@
 // write_kv_token / write_kv_prefill (src/kv_cache_manager.cpp:297-314,
 // src/paged_attention.cpp:127-168).
 //
-// One wave per (token, kv head).  Encodings:
+// One wave per (token, kv head) in general; a vector path (16-byte loads,
+// several rows per wave) when head_dim % 4 == 0 and the pages are aligned.
+// Encodings:
 //   fp32  copied;
 //   fp16  the reference encoder (src/kv_cache_manager.cpp:157-179): mantissa
 //         truncated, exponents below the fp16 normal range flushed to +/-0,
@@ -128,11 +130,89 @@ __global__ __launch_bounds__(256) void kv_write_kernel(KvWriteParams p) {
     }
 }
 
+// Vector path (head_dim % 4 == 0, aligned pages): a row of one (token, kv
+// head) is owned by L = head_dim / 4 consecutive lanes, 4 values each (one
+// 16-byte load per lane and K/V), rows_per_wave = 64 / L rows per wave.  Same
+// encodings as kv_write_kernel; int8 forms the row's max |x| across its lane
+// segment.
+template <int KV>
+__global__ __launch_bounds__(256) void kv_write_vec_kernel(KvWriteParams p, int L, int rows_per_wave) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int seg = lane / L, li = lane - seg * L;
+    if (seg >= rows_per_wave) return;  // whole segments idle
+    const int64_t item = ((int64_t)blockIdx.x * 4 + wave) * rows_per_wave + seg;
+    if (item >= (int64_t)p.num_tokens * p.num_kv_heads) return;
+    const int64_t tok = item / p.num_kv_heads;
+    const int h = (int)(item - tok * p.num_kv_heads);
+    const int64_t slot = p.slots[tok];
+    if (slot < 0) return;
+    const int64_t block = slot / p.block_size;
+    if (block >= p.num_blocks) return;
+    const int pos = (int)(slot - block * p.block_size);
+    const int D = p.head_dim;
+    const int64_t src_off = (tok * p.num_kv_heads + h) * D + 4 * li;
+    const int64_t dst_off = block * p.block_stride + ((int64_t)pos * p.num_kv_heads + h) * D + 4 * li;
+    for (int which = 0; which < 2; ++which) {
+        const float4 x = *reinterpret_cast<const float4*>((which ? p.v_src : p.k_src) + src_off);
+        void* base = which ? p.v : p.k;
+        if constexpr (KV == VCPP_KV_F32) {
+            *reinterpret_cast<float4*>(static_cast<float*>(base) + dst_off) = x;
+        } else if constexpr (KV == VCPP_KV_F16) {
+            uint16_t e[4];
+            const float xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) e[i] = p.fp16_rne ? f16_rne(xs[i]) : f16_trunc(xs[i]);
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(base) + dst_off) =
+                make_uint2(e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16));
+        } else if constexpr (KV == VCPP_KV_FP8) {
+            const uint32_t w = fp8_encode(x.x) | ((uint32_t)fp8_encode(x.y) << 8) |
+                               ((uint32_t)fp8_encode(x.z) << 16) | ((uint32_t)fp8_encode(x.w) << 24);
+            *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(base) + dst_off) = w;
+        } else {
+            float amax = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+            float row_max = amax;
+            for (int j = 0; j < L; ++j) row_max = fmaxf(row_max, __shfl(amax, seg * L + j, 64));
+            const uint16_t sh = f16_rne(row_max / 127.0f);
+            const float sc = f16_to_f32(sh);
+            const float xs[4] = {x.x, x.y, x.z, x.w};
+            uint32_t w = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float r = sc > 0.0f ? rintf(xs[i] / sc) : 0.0f;
+                r = fminf(fmaxf(r, -127.0f), 127.0f);
+                w |= (uint32_t)(uint8_t)(int8_t)r << (8 * i);
+            }
+            *reinterpret_cast<uint32_t*>(static_cast<int8_t*>(base) + dst_off) = w;
+            if (li == 0) {
+                uint16_t* scp = which ? p.v_scale : p.k_scale;
+                scp[block * p.scale_block_stride + (int64_t)h * p.block_size + pos] = sh;
+            }
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_kv_write(const KvWriteParams& p, hipStream_t stream) {
     const int64_t items = (int64_t)p.num_tokens * p.num_kv_heads;
     if (items == 0) return hipSuccess;
+    const int es = p.dtype == VCPP_KV_F32 ? 4 : p.dtype == VCPP_KV_F16 ? 2 : 1;
+    auto aligned = [](const void* q, int a) { return (reinterpret_cast<uintptr_t>(q) % a) == 0; };
+    const bool vec = p.head_dim % 4 == 0 && p.head_dim <= 256 && p.block_stride % 4 == 0 &&
+                     aligned(p.k_src, 16) && aligned(p.v_src, 16) && aligned(p.k, 4 * es) &&
+                     aligned(p.v, 4 * es);
+    if (vec) {
+        const int L = p.head_dim / 4, rpw = 64 / L;
+        const int64_t waves = (items + rpw - 1) / rpw;
+        const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+        switch (p.dtype) {
+            case VCPP_KV_F32: hipLaunchKernelGGL(kv_write_vec_kernel<VCPP_KV_F32>, grid, block, 0, stream, p, L, rpw); break;
+            case VCPP_KV_F16: hipLaunchKernelGGL(kv_write_vec_kernel<VCPP_KV_F16>, grid, block, 0, stream, p, L, rpw); break;
+            case VCPP_KV_FP8: hipLaunchKernelGGL(kv_write_vec_kernel<VCPP_KV_FP8>, grid, block, 0, stream, p, L, rpw); break;
+            default: hipLaunchKernelGGL(kv_write_vec_kernel<VCPP_KV_I8>, grid, block, 0, stream, p, L, rpw); break;
+        }
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(kv_write_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
