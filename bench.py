@@ -352,10 +352,35 @@ def cpu_baseline(torch, w, target_s):
         run()
         dt += time.perf_counter() - t0
         reps += 1
-    return {"value": reps * w["bytes"] / dt / 1e12, "unit": "TB/s", "cores": cores, "kind": kind,
-            "sample": "the full config-2 batch (64 seqs, %d context tokens) x %d repetitions, "
-                      "paged_attention() per sequence on an FP32 pool holding the decoded fp16 "
-                      "values, %.1f s" % (w["total_tokens"], reps, dt)}
+    out = {"value": reps * w["bytes"] / dt / 1e12, "unit": "TB/s", "cores": cores, "kind": kind,
+           "sample": "the full config-2 batch (64 seqs, %d context tokens) x %d repetitions, "
+                     "paged_attention() per sequence on an FP32 pool holding the decoded fp16 "
+                     "values, %.1f s" % (w["total_tokens"], reps, dt)}
+    return out
+
+
+def cpu_port_threaded(torch, w, target_s):
+    """The build's own CPU restatement (oracle/oracle.c, orc_decode_batch)
+    threaded over (sequence, head) on the host's cores (at most 16, the box's
+    CPU share), on the same config-2 batch."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    k, v, tables = w["sets"][0]
+    pool = O.Pool(O.ORC_F32, k.float().cpu().numpy(), v.float().cpu().numpy())
+    tables = tables.cpu().numpy()
+    ctx = w["ctx"].numpy().astype(np.int32)
+    q = w["q"].cpu().numpy()
+    cores = max(1, min(16, os.cpu_count() or 1))
+    reps, dt = 0, 0.0
+    while dt < target_s and reps < 1000:
+        t0 = time.perf_counter()
+        O.decode(pool, q, tables, ctx, H, nthreads=cores)
+        dt += time.perf_counter() - t0
+        reps += 1
+    return {"value": reps * w["bytes"] / dt / 1e12, "unit": "TB/s", "cores": cores, "kind": "port",
+            "sample": "the full config-2 batch x %d repetitions, oracle threaded over (sequence, head), "
+                      "%.1f s" % (reps, dt)}
 
 
 def read_traffic(name):
@@ -602,6 +627,7 @@ def main():
         result["kv_write"] = bench_kvwrite(torch, pyvcpp, args)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(torch, w, args.cpu_seconds)
+        result["cpu_port_threaded"] = cpu_port_threaded(torch, w, min(args.cpu_seconds, 5.0))
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result))
