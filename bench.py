@@ -600,7 +600,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16 KV / fp32 q,out, fp32 accumulate",
+        "dtype": "f16",
+        "dtype_note": "f16 K/V pages and MFMA operands (q split hi/lo), fp32 accumulate, fp32 q/out",
         "data": "synthetic (seeded N(0,1) q/K/V, random block tables)",
         "config": {"workload": "BASELINE config 2: batched paged decode, 64 seqs, ctx U[128,4096], "
                                "64 q / 8 kv heads, head_dim 80, fp16 pages of 16 tokens, pool 1.25x",
