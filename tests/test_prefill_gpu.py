@@ -98,3 +98,32 @@ def test_prefill_config3_sampled(cuda):
                                      q_start[1:] - 1]))
     want = oracle_prefill_rows(pool, q32, tables, q_start, pre, 64, rows)
     assert_close(got[rows], want, ATOL, RTOL, what="config3 rows")
+
+
+@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8, O.ORC_FP8])
+def test_prefill_block_size_32(cuda, kind):
+    """Pages of 32 tokens: a 32-key block is one whole page, and chunk
+    boundaries fall inside pages."""
+    bs, H, Hkv, D = 32, 16, 2, 80
+    prefix, chunk = [45, 0, 130], [70, 33, 17]
+    lens = [p + n for p, n in zip(prefix, chunk)]
+    nb = sum((l + bs - 1) // bs for l in lens) + 3
+    shape = (nb, bs, Hkv, D)
+    k = O.normal(301, shape)
+    v = O.normal(302, shape)
+    if kind == O.ORC_F16:
+        pool = O.Pool(kind, O.f16_trunc(k), O.f16_trunc(v), block_size=bs)
+    elif kind == O.ORC_FP8:
+        pool = O.Pool(kind, O.fp8_encode(k), O.fp8_encode(v), block_size=bs)
+    else:
+        kq, ks = O.quant_i8(k)
+        vq, vs = O.quant_i8(v)
+        pool = O.Pool(kind, kq, vq, np.ascontiguousarray(ks.transpose(0, 2, 1)),
+                      np.ascontiguousarray(vs.transpose(0, 2, 1)), block_size=bs)
+    q_start = np.concatenate([[0], np.cumsum(chunk)]).astype(np.int32)
+    q16 = O.normal(303, (int(q_start[-1]), H, D)).astype(np.float16)
+    tables = prefill_tables(304, lens, nb, bs=bs)
+    pre = np.array(prefix, np.int32)
+    want = O.prefill(pool, q16.astype(np.float32), tables, q_start, pre, H)
+    got = gpu_prefill(DevPool(pool), q16.view(np.uint16), tables, q_start, pre, H)
+    assert_close(got, want, ATOL, RTOL, what="prefill block_size 32 kind=%d" % kind)
