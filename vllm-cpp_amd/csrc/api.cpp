@@ -115,9 +115,10 @@ DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_he
                    vcpp::decode_page_mode_supported(kv->dtype, kv->num_kv_heads, group, D,
                                                     kv->block_size);
     // Ranges that are all resident at once: 2 waves per SIMD, 4 SIMDs per CU
-    // (page mode: one 8-wave workgroup per CU covers every kv head).
+    // (page mode: 8-wave workgroups that each cover every kv head, one per CU
+    // for fp16 pages and two for byte pages).
     const int64_t slots = (int64_t)device_cus() * (8 / wpw);
-    int64_t G = pl.page_mode ? device_cus() : slots / groups;
+    int64_t G = pl.page_mode ? (int64_t)device_cus() * vcpp::decode_page_wg_per_cu(kv->dtype) : slots / groups;
     const int64_t tiles_upper = (int64_t)num_seqs * ((max_context_len + 15) / 16);
     if (partition_size > 0) {
         G = (tiles_upper * 16 + partition_size - 1) / partition_size;

@@ -816,14 +816,18 @@ struct PageCfg {
     static constexpr int NREAL = 2 * NI + (SCALED ? 1 : 0);  // + the scale instruction
     static constexpr int PERW = (NREAL + kPageWaves - 1) / kPageWaves;
     static constexpr int STAGE = 2 * REG + (SCALED ? 1024 : 0);
-    // byte tiles carry half the bytes: twice the tiles in flight.
-    static constexpr int STAGES = BYTES ? 5 : 3;
+    // Byte pages run two workgroups per CU (4 waves per SIMD, a 3-tile ring
+    // each): the second workgroup's waves hide the per-tile latency of the
+    // first, which a deeper single ring does not.  fp16 tiles are twice the
+    // bytes and need the whole LDS for 3 tiles.
+    static constexpr int WPC = BYTES ? 2 : 1;   // workgroups per CU
+    static constexpr int WPE = 2 * WPC;         // waves per SIMD
+    static constexpr int STAGES = 3;
     static constexpr int OFF_JUNK = STAGES * STAGE;       // target of padding DMAs
-    static constexpr int OFF_VT = OFF_JUNK + (PERW * kPageWaves > NREAL ? 1024 : 0);
-    static constexpr int OFF_LIST = OFF_VT + (BYTES ? kPageWaves * 16 * D * 2 : 0);
+    static constexpr int OFF_LIST = OFF_JUNK + (PERW * kPageWaves > NREAL ? 1024 : 0);
     static constexpr int LDS = OFF_LIST + kPageWindow * (int)sizeof(PageEntry);
     static_assert(RC % SWZ == 0 && REG % 1024 == 0 && (D * ES) % 16 == 0, "tile shape");
-    static_assert(LDS <= 160 * 1024, "LDS budget");
+    static_assert(LDS * WPC <= 160 * 1024, "LDS budget");
 };
 
 __device__ __attribute__((aligned(16))) const uint32_t kZeroChunk16[4] = {0, 0, 0, 0};
@@ -848,7 +852,7 @@ __device__ __forceinline__ int page_slot(int gc, int rc) {
 }
 
 template <int KV, int D>
-__global__ __launch_bounds__(kPageWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(kPageWaves * 64) __attribute__((amdgpu_waves_per_eu(PageCfg<KV, D>::WPE, PageCfg<KV, D>::WPE)))
 void decode_page_kernel(DecodeParams p) {
     using C = PageCfg<KV, D>;
     constexpr bool BYTES = C::BYTES, SCALED = C::SCALED;
@@ -1023,7 +1027,6 @@ void decode_page_kernel(DecodeParams p) {
     };
     typedef __attribute__((address_space(3))) uint32_t lds_u32;
     typedef __attribute__((address_space(3))) i2 lds_i2;
-    lds_char* vt = lds + C::OFF_VT + wave * 16 * D * 2;  // byte pages: this wave's fp16 V tile
 
     auto compute_tile = [&](int tau, const PageEntry& e) {
         lds_char* sb = lds + (tau % STAGES) * STAGE;
@@ -1046,18 +1049,6 @@ void decode_page_kernel(DecodeParams p) {
                 const uint32_t kw = *reinterpret_cast<lds_u32*>(sb + kofs(2 * NC32) + 4 * g);
                 const f4 zero = {0.f, 0.f, 0.f, 0.f};
                 acc += mfma16(bytes4_to_h4<KV>(kw), qr, zero);
-            }
-            // widen V rows of token c into the wave's row-major [16][D] fp16 tile
-#pragma unroll
-            for (int cc = 0; cc < NC32; ++cc) {
-                const i2 vw = *reinterpret_cast<lds_i2*>(sb + REG + kofs(2 * cc + (g >> 1)) + 8 * (g & 1));
-                *reinterpret_cast<__attribute__((address_space(3))) h8*>(vt + (c * D + 32 * cc + 8 * g) * 2) =
-                    bytes8_to_h8<KV>((uint32_t)vw.x, (uint32_t)vw.y);
-            }
-            if constexpr (Dims<D>::REM) {
-                const uint32_t vw = *reinterpret_cast<lds_u32*>(sb + REG + kofs(2 * NC32) + 4 * g);
-                *reinterpret_cast<__attribute__((address_space(3))) h4*>(vt + (c * D + 32 * NC32 + 4 * g) * 2) =
-                    bytes4_to_h4<KV>(vw);
             }
         } else {
 #pragma unroll
@@ -1114,17 +1105,30 @@ void decode_page_kernel(DecodeParams p) {
             const _Float16 hi = (_Float16)pr;
             pa[r] = c < 8 ? hi : (_Float16)(pr - (float)hi);
         }
+        if constexpr (BYTES) {
+            // One ds_read_b64_tr_b8 per pair of output blocks (t, t+1): lane
+            // i of each 16-lane group gets byte i mod 8 of the read of lane
+            // 2j + i/8, j = 0..7.  Lanes 2j, 2j+1 of group g read token
+            // 4g + (j & 3), dims 16u .. 16u+15 of head kvh (one 16-byte
+            // chunk), u = t for j < 4 and t+1 above, so lane (g, c) gets
+            // V[4g + r][16t + c] in bytes r and V[4g + r][16(t+1) + c] in
+            // bytes 4 + r.  An odd last block reads itself twice.
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            h4 vf;
-            if constexpr (BYTES) {
-                vf = read_v_tr<D>(vt, t, g, c);
-            } else {
+            for (int t = 0; t < NT; t += 2) {
+                const int j = c >> 1;
+                const int u = (j < 4 || t + 1 == NT) ? t : t + 1;
+                const int ofs = REG + page_slot<SWZ>((4 * g + (j & 3)) * RC + kvh * HC + u, RC) * 16 + 8 * (c & 1);
+                const i2 x = __builtin_amdgcn_ds_read_tr8_b64_v2i32(reinterpret_cast<lds_i2*>(sb + ofs));
+                o[t] = mfma16(pa, bytes4_to_h4<KV>((uint32_t)x.x), o[t]);
+                if (t + 1 < NT) o[t + 1] = mfma16(pa, bytes4_to_h4<KV>((uint32_t)x.y), o[t + 1]);
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
                 const s4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                     reinterpret_cast<__attribute__((address_space(3))) s4*>(sb + vofs(t)));
-                vf = __builtin_bit_cast(h4, x);
+                o[t] = mfma16(pa, __builtin_bit_cast(h4, x), o[t]);
             }
-            o[t] = mfma16(pa, vf, o[t]);
         }
         l_run = l_run * alpha + lsum;
     };
@@ -1301,6 +1305,10 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
     err = hipGetLastError();
     if (prof) prof_end(kKernelMerge, stream);
     return err;
+}
+
+int decode_page_wg_per_cu(int kv_dtype) {
+    return kv_dtype == VCPP_KV_I8 || kv_dtype == VCPP_KV_FP8 ? 2 : 1;
 }
 
 bool decode_page_mode_supported(int kv_dtype, int num_kv_heads, int group, int head_dim,
