@@ -37,6 +37,7 @@ namespace {
 constexpr int kKBlk = 32;   // keys per block
 constexpr int kHeadsPerGroup = 4;
 constexpr float kLazy = 8.0f;  // log2 of the largest P allowed before rescaling
+constexpr float kLazyP = 256.0f;  // 2^kLazy
 
 typedef short s4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -350,15 +351,13 @@ void prefill_dma_kernel(PrefillParams p) {
         for (int t = 0; t < NT; ++t) o[rb][t] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) lsum[rb] = 0.f;
-    // Running max per row (log2 units) and the per-lane score above which a
-    // rescale is due: raw scores against (m + 2^8) / scale (fp16 pages), or
-    // already scaled scores (int8 pages) against m + 2^8.
+    // Running max per row (log2 units); int8 pages also keep the scaled
+    // score above which a rescale is due (m + kLazy).
     float m_run[RB], thr[RB];
-    const float inv_scale = 1.0f / p.scale_log2;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
         m_run[rb] = kMaxSeed;
-        thr[rb] = SCALED ? kMaxSeed + kLazy : (kMaxSeed + kLazy) * inv_scale;
+        thr[rb] = kMaxSeed + kLazy;
     }
 
     // LDS byte offsets of this lane's fragment reads: one base each plus
@@ -415,11 +414,10 @@ void prefill_dma_kernel(PrefillParams p) {
                 tile_ok[kt] = k16 < tab_end && table_s[lb] >= 0;
             }
         }
-        // Row blocks go in groups of SG: S^T of a group, one ballot over the
-        // group (does any row need its running max moved?), then exp and P V.
-        // fp16 pages: raw S, scaled and shifted per element in one fma;
-        // int8 pages: S times the key's scale (log2 units).
-        auto s_group = [&](int rb0, float (&sc)[SG][2][4], float (&mx)[SG]) {
+        // Row blocks go in groups of SG.  fp16 P: raw S, scaled and shifted per
+        // element in one fma; int8 pages: S times the key's scale (log2 units),
+        // max checked before the exp (check_group, p_group, pv_group).
+        auto s_group = [&](int rb0, float (&sc)[SG][2][4], float* mx) {
             float ks[2][4];  // int8: K scales times log2(e) / sqrt(D)
             if constexpr (SCALED) {
                 scales(0, ks);
@@ -449,9 +447,10 @@ void prefill_dma_kernel(PrefillParams p) {
                         sc[i][kt][r] = x;
                     }
                 }
-                mx[i] = vmax(vmax3(sc[i][0][0], sc[i][0][1], sc[i][0][2]),
-                             vmax3(sc[i][0][3], sc[i][1][0], sc[i][1][1]),
-                             vmax3(sc[i][1][2], sc[i][1][3], sc[i][1][3]));
+                if (mx)
+                    mx[i] = vmax(vmax3(sc[i][0][0], sc[i][0][1], sc[i][0][2]),
+                                 vmax3(sc[i][0][3], sc[i][1][0], sc[i][1][1]),
+                                 vmax3(sc[i][1][2], sc[i][1][3], sc[i][1][3]));
             }
         };
         // Per-lane test against the threshold; the row max over the four
@@ -466,19 +465,10 @@ void prefill_dma_kernel(PrefillParams p) {
                     const int rb = rb0 + i;
                     const float mr = max_over_groups(mx[i]);
                     const bool grow = mr > thr[rb];  // uniform per row
-                    float alpha;
-                    if constexpr (SCALED) {
-                        const float m_new = grow ? mr : m_run[rb];
-                        alpha = fast_exp2(m_run[rb] - m_new);
-                        m_run[rb] = m_new;
-                        thr[rb] = m_new + kLazy;
-                    } else {
-                        const float ml = mr * p.scale_log2;
-                        const float m_new = grow ? ml : m_run[rb];
-                        alpha = fast_exp2(m_run[rb] - m_new);
-                        m_run[rb] = m_new;
-                        thr[rb] = (m_new + kLazy) * inv_scale;
-                    }
+                    const float m_new = grow ? mr : m_run[rb];
+                    const float alpha = fast_exp2(m_run[rb] - m_new);
+                    m_run[rb] = m_new;
+                    thr[rb] = m_new + kLazy;
                     lsum[rb] *= alpha;  // row c: this lane's own
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
@@ -489,60 +479,108 @@ void prefill_dma_kernel(PrefillParams p) {
                 }
             }
         };
+        // P (fp32) into the row sum; P times the V scale, rounded once,
+        // weights the int8 V values.
         auto p_group = [&](int rb0, const float (&sc)[SG][2][4], h8 (&pa)[SG]) {
-            float vs[2][4];  // int8: V scales
-            if constexpr (SCALED) scales(1, vs);
+            float vs[2][4];
+            scales(1, vs);
 #pragma unroll
             for (int i = 0; i < SG; ++i)
 #pragma unroll
                 for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        if constexpr (SCALED) {
-                            // P (fp32) into the row sum; P times the V scale,
-                            // rounded once, weights the int8 V values.
-                            const float pr = fast_exp2(sc[i][kt][r] - m_run[rb0 + i]);
-                            lsum[rb0 + i] += pr;
-                            pa[i][4 * kt + r] = (_Float16)(pr * vs[kt][r]);
-                        } else
-                            pa[i][4 * kt + r] =
-                                (_Float16)fast_exp2(fmaf(sc[i][kt][r], p.scale_log2, -m_run[rb0 + i]));
+                        const float pr = fast_exp2(sc[i][kt][r] - m_run[rb0 + i]);
+                        lsum[rb0 + i] += pr;
+                        pa[i][4 * kt + r] = (_Float16)(pr * vs[kt][r]);
                     }
         };
         auto pv_group = [&](int rb0, const h8 (&pa)[SG]) {
 #pragma unroll
-            for (int i = 0; i < SG; ++i) {
+            for (int i = 0; i < SG; ++i)
 #pragma unroll
                 for (int t = 0; t < NT; ++t) o[rb0 + i][t] = mfma32(pa[i], vb[t], o[rb0 + i][t]);
-                if constexpr (!SCALED) {  // row sums of exactly the fp16 P that weights V
+        };
+        if constexpr (SCALED) {
+            // int8: S, max check, exp, P V, one group after the other.
+            float sc[2][SG][2][4], mx[2][SG];
+            h8 pa[SG];
+            s_group(0, sc[0], mx[0]);
+            check_group(0, sc[0], mx[0]);
 #pragma unroll
-                    for (int e = 0; e < 8; e += 2)
-                        lsum[rb0 + i] =
-                            __builtin_amdgcn_fdot2(h2{pa[i][e], pa[i][e + 1]}, h2{1, 1}, lsum[rb0 + i], false);
+            for (int j = 0; j < RB / SG; ++j) {
+                const bool more = j + 1 < RB / SG;
+                const int nx = (j + 1) & 1;
+                p_group(j * SG, sc[j & 1], pa);
+                pv_group(j * SG, pa);
+                if (more) s_group((j + 1) * SG, sc[nx], mx[nx]);
+                if (more) check_group((j + 1) * SG, sc[nx], mx[nx]);
+            }
+        } else {
+            // fp16 P: exp first, check after.  With the running max m, a
+            // score past the lazy threshold (m + kLazy in log2 units) has
+            // P > 2^kLazy, and one far past it overflows fp16 to inf, so the
+            // lane's block sum of P -- which the row sum needs anyway --
+            // exceeds 2^kLazy whenever a row of the lane must be rescaled
+            // (rarely otherwise).  Only then is the row max formed, and the
+            // group's P recomputed if the max moved.  The exp of group j runs
+            // under the S^T MFMAs of group j + 1.
+            float sc[2][SG][2][4];
+            h8 pa[SG];
+            float bs[SG];
+            auto p_sum = [&](int i, int rb, const float (&sci)[2][4]) {
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        pa[i][4 * kt + r] = (_Float16)fast_exp2(fmaf(sci[kt][r], p.scale_log2, -m_run[rb]));
+                float b = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; e += 2)
+                    b = __builtin_amdgcn_fdot2(h2{pa[i][e], pa[i][e + 1]}, h2{1, 1}, b, false);
+                bs[i] = b;
+            };
+            s_group(0, sc[0], nullptr);
+#pragma unroll
+            for (int j = 0; j < RB / SG; ++j) {
+                const bool more = j + 1 < RB / SG;
+                const int nx = (j + 1) & 1;
+#pragma unroll
+                for (int i = 0; i < SG; ++i) p_sum(i, j * SG + i, sc[j & 1][i]);
+                if (more) s_group((j + 1) * SG, sc[nx], nullptr);
+                bool cross = false;
+#pragma unroll
+                for (int i = 0; i < SG; ++i) cross |= !(bs[i] <= kLazyP);  // inf and NaN too
+                if (__builtin_expect(__any(cross), 0)) {
+#pragma unroll
+                    for (int i = 0; i < SG; ++i) {
+                        const int rb = j * SG + i;
+                        const float (&sci)[2][4] = sc[j & 1][i];
+                        const float mr = max_over_groups(vmax(vmax3(sci[0][0], sci[0][1], sci[0][2]),
+                                                              vmax3(sci[0][3], sci[1][0], sci[1][1]),
+                                                              vmax3(sci[1][2], sci[1][3], sci[1][3])));
+                        const float ml = mr * p.scale_log2;
+                        const bool grow = ml > m_run[rb] + kLazy;  // uniform per row
+                        const float m_new = grow ? ml : m_run[rb];
+                        const float alpha = fast_exp2(m_run[rb] - m_new);
+                        m_run[rb] = m_new;
+                        lsum[rb] *= alpha;  // row c: this lane's own
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float a = shfl(alpha, 4 * g + r);
+#pragma unroll
+                            for (int t = 0; t < NT; ++t) o[rb][t][r] *= a;
+                        }
+                        if (__any(grow)) p_sum(i, rb, sci);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < SG; ++i) {
+                    lsum[j * SG + i] += bs[i];
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) o[j * SG + i][t] = mfma32(pa[i], vb[t], o[j * SG + i][t]);
                 }
             }
-        };
-        // fp16: two-stage software pipeline over the groups -- the exp of
-        // group j runs under the S^T MFMAs of group j + 1, and the P V MFMAs
-        // of group j under the max of group j + 1.  int8 (more live scale
-        // state) takes the groups one after the other.
-        float sc[2][SG][2][4], mx[2][SG];
-        h8 pa[SG];
-        s_group(0, sc[0], mx[0]);
-        check_group(0, sc[0], mx[0]);
-#pragma unroll
-        for (int j = 0; j < RB / SG; ++j) {
-            const bool more = j + 1 < RB / SG;
-            const int nx = (j + 1) & 1;
-            p_group(j * SG, sc[j & 1], pa);
-            if constexpr (!SCALED) {
-                if (more) s_group((j + 1) * SG, sc[nx], mx[nx]);
-                pv_group(j * SG, pa);
-            } else {
-                pv_group(j * SG, pa);
-                if (more) s_group((j + 1) * SG, sc[nx], mx[nx]);
-            }
-            if (more) check_group((j + 1) * SG, sc[nx], mx[nx]);
         }
     };
 
