@@ -108,10 +108,9 @@ struct ByteDims {
     static_assert((2 * REGION) % 64 == 0, "byte stage must be whole DMA instructions");
 };
 
-// Query row blocks per wave: 4 (2 for D = 128) with fp16 and FP8 pages; int8
-// pages carry per-key scale state and use 2.
+// Query row blocks per wave: 4 (2 for D = 128).
 template <int KV, int D>
-constexpr int rows_blocks() { return KV == VCPP_KV_I8 ? 2 : PDims<D>::RB; }
+constexpr int rows_blocks() { return PDims<D>::RB; }
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -170,7 +169,7 @@ void prefill_dma_kernel(PrefillParams p) {
     constexpr int AREA = kStages * RSTAGE;
     constexpr int NF16 = BYTES ? 2 : kStages;       // fp16-format stages
     constexpr int F16BASE = BYTES ? AREA : 0;
-    constexpr int SG = 2;  // row blocks per softmax group
+    constexpr int SG = SCALED ? 1 : 2;  // row blocks per softmax group (int8: registers)
     constexpr int NC32 = PDims<D>::NC32, NT = PDims<D>::NT;
     constexpr int RB = rows_blocks<KV, D>();  // 16-row blocks per wave
     constexpr int kQTile = 16 * RB;
@@ -318,9 +317,21 @@ void prefill_dma_kernel(PrefillParams p) {
             }
         }
     };
-    // Blocks kb, kb + 1 (int8 ring) -> the fp16 area as exact fp16 integers;
-    // the per-key scales are applied in fp32 to the scores (K) and to P (V).
+    // Blocks kb, kb + 1 (byte ring) -> the fp16 area.  FP8: the values.
+    // int8: K as exact fp16 integers, its per-key scale times log2(e)/sqrt(D)
+    // converted in place to fp32 for the exp's fma (at least FLT_MIN, so a
+    // masked key's -inf never meets a zero scale); V times its key's scale,
+    // one IEEE fp16 rounding of the exact product (v_pk_mul_f16).
     auto widen = [&](int kb) {
+        if constexpr (SCALED) {
+            if (tid < 64) {
+                lds_char* sw = lds + ((kb + (tid >> 5)) % kStages) * RSTAGE + ID::SCALES + (tid & 31) * 4;
+                const float ks = (float)__builtin_bit_cast(
+                    _Float16, *reinterpret_cast<__attribute__((address_space(3))) const uint16_t*>(sw));
+                *reinterpret_cast<__attribute__((address_space(3))) float*>(sw) =
+                    fmaxf(ks * p.scale_log2, 1.17549435e-38f);
+            }
+        }
 #pragma unroll
         for (int u0 = 0; u0 < 2 * ID::UNITS; u0 += 256) {
             const int u = u0 + tid;
@@ -332,8 +343,16 @@ void prefill_dma_kernel(PrefillParams p) {
                 const int ch = q >> 5, key = q & 31;
                 lds_char* st = lds + ((kb + blk) % kStages) * RSTAGE;
                 const i4 raw = *reinterpret_cast<__attribute__((address_space(3))) i4*>(st + v * 16);
-                const h8 lo = bytes8_to_h8<KV>((uint32_t)raw.x, (uint32_t)raw.y);
-                const h8 hi = bytes8_to_h8<KV>((uint32_t)raw.z, (uint32_t)raw.w);
+                h8 lo = bytes8_to_h8<KV>((uint32_t)raw.x, (uint32_t)raw.y);
+                h8 hi = bytes8_to_h8<KV>((uint32_t)raw.z, (uint32_t)raw.w);
+                if constexpr (SCALED) {
+                    if (which) {  // V scale dword of the key: fp16 in the low half
+                        const _Float16 sc = __builtin_bit_cast(_Float16, *reinterpret_cast<
+                            __attribute__((address_space(3))) const uint16_t*>(st + ID::SCALES + (32 + key) * 4));
+                        lo *= sc;
+                        hi *= sc;
+                    }
+                }
                 lds_char* dst = lds + AREA + blk * DD::STAGE + which * DD::REGION * 16;
                 *reinterpret_cast<__attribute__((address_space(3))) h8*>(dst + slot_of(2 * ch, key) * 16) = lo;
                 *reinterpret_cast<__attribute__((address_space(3))) h8*>(dst + slot_of(2 * ch + 1, key) * 16) = hi;
@@ -351,14 +370,10 @@ void prefill_dma_kernel(PrefillParams p) {
         for (int t = 0; t < NT; ++t) o[rb][t] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) lsum[rb] = 0.f;
-    // Running max per row (log2 units); int8 pages also keep the scaled
-    // score above which a rescale is due (m + kLazy).
-    float m_run[RB], thr[RB];
+    // Running max per row (log2 units).
+    float m_run[RB];
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-        m_run[rb] = kMaxSeed;
-        thr[rb] = kMaxSeed + kLazy;
-    }
+    for (int rb = 0; rb < RB; ++rb) m_run[rb] = kMaxSeed;
 
     // LDS byte offsets of this lane's fragment reads: one base each plus
     // compile-time offsets.  K row 16 kt + c of chunk 4 cc + g sits in slot
@@ -394,17 +409,6 @@ void prefill_dma_kernel(PrefillParams p) {
             const h4 hi = read_tr(sb + vbase + (64 * t + 16) * 16);
             vb[t] = h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
-        // int8: per-key scales of this lane's keys 16 kt + 4 g + r (K's at
-        // which = 0, V's at which = 1), read where they are used.
-        auto scales = [&](int which, float (&sv)[2][4]) {
-            lds_char* scl = lds + (kb % kStages) * RSTAGE + ID::SCALES + which * 32 * 4;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
-                const i4 w = *reinterpret_cast<__attribute__((address_space(3))) i4*>(scl + (16 * kt + 4 * g) * 4);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) sv[kt][r] = (float)__builtin_bit_cast(_Float16, (uint16_t)w[r]);
-            }
-        };
         bool tile_ok[2] = {true, true};
         if constexpr (MASKED) {
 #pragma unroll
@@ -414,18 +418,9 @@ void prefill_dma_kernel(PrefillParams p) {
                 tile_ok[kt] = k16 < tab_end && table_s[lb] >= 0;
             }
         }
-        // Row blocks go in groups of SG.  fp16 P: raw S, scaled and shifted per
-        // element in one fma; int8 pages: S times the key's scale (log2 units),
-        // max checked before the exp (check_group, p_group, pv_group).
-        auto s_group = [&](int rb0, float (&sc)[SG][2][4], float* mx) {
-            float ks[2][4];  // int8: K scales times log2(e) / sqrt(D)
-            if constexpr (SCALED) {
-                scales(0, ks);
-#pragma unroll
-                for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) ks[kt][r] *= p.scale_log2;
-            }
+        // Row blocks go in groups of SG: raw S^T, then exp of the scaled,
+        // shifted scores (one fma each) and P V.
+        auto s_group = [&](int rb0, float (&sc)[SG][2][4]) {
 #pragma unroll
             for (int i = 0; i < SG; ++i) {
                 const int rb = rb0 + i;
@@ -438,7 +433,6 @@ void prefill_dma_kernel(PrefillParams p) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         float x = acc[r];
-                        if constexpr (SCALED) x *= ks[kt][r];
                         if constexpr (MASKED) {
                             const int key = key0 + 16 * kt + 4 * g + r;
                             const int lim = min(prefix + t0 + 16 * rb + c, kv_end - 1);
@@ -447,28 +441,78 @@ void prefill_dma_kernel(PrefillParams p) {
                         sc[i][kt][r] = x;
                     }
                 }
-                if (mx)
-                    mx[i] = vmax(vmax3(sc[i][0][0], sc[i][0][1], sc[i][0][2]),
-                                 vmax3(sc[i][0][3], sc[i][1][0], sc[i][1][1]),
-                                 vmax3(sc[i][1][2], sc[i][1][3], sc[i][1][3]));
             }
         };
-        // Per-lane test against the threshold; the row max over the four
-        // lane groups is only formed when some lane crossed it.
-        auto check_group = [&](int rb0, float (&sc)[SG][2][4], const float (&mx)[SG]) {
+        // Exp first, check after.  With the running max m, a
+        // score past the lazy threshold (m + kLazy in log2 units) has
+        // P > 2^kLazy, and one far past it overflows fp16 to inf, so the
+        // lane's block sum of P -- which the row sum needs anyway --
+        // exceeds 2^kLazy whenever a row of the lane must be rescaled
+        // (rarely otherwise).  Only then is the row max formed, and the
+        // group's P recomputed if the max moved.  The exp of group j runs
+        // under the S^T MFMAs of group j + 1.
+        float sc[2][SG][2][4];
+        h8 pa[SG];
+        float bs[SG];
+        // Score scale of this lane's keys 16 kt + 4 g + r: log2(e)/sqrt(D),
+        // times the key's scale on int8 pages (read where it is used).
+        auto score_scale = [&](float (&ksc)[2][4]) {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                if constexpr (SCALED) {
+                    const f4 w = *reinterpret_cast<__attribute__((address_space(3))) const f4*>(
+                        lds + (kb % kStages) * RSTAGE + ID::SCALES + (16 * kt + 4 * g) * 4);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) ksc[kt][r] = w[r];
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) ksc[kt][r] = p.scale_log2;
+                }
+            }
+        };
+        auto p_sum = [&](int i, int rb, const float (&sci)[2][4]) {
+            float ksc[2][4];
+            score_scale(ksc);
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    pa[i][4 * kt + r] = (_Float16)fast_exp2(fmaf(sci[kt][r], ksc[kt][r], -m_run[rb]));
+            float b = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; e += 2)
+                b = __builtin_amdgcn_fdot2(h2{pa[i][e], pa[i][e + 1]}, h2{1, 1}, b, false);
+            bs[i] = b;
+        };
+        s_group(0, sc[0]);
+#pragma unroll
+        for (int j = 0; j < RB / SG; ++j) {
+            const bool more = j + 1 < RB / SG;
+            const int nx = (j + 1) & 1;
+#pragma unroll
+            for (int i = 0; i < SG; ++i) p_sum(i, j * SG + i, sc[j & 1][i]);
+            if (more) s_group((j + 1) * SG, sc[nx]);
             bool cross = false;
 #pragma unroll
-            for (int i = 0; i < SG; ++i) cross |= mx[i] > thr[rb0 + i];
+            for (int i = 0; i < SG; ++i) cross |= !(bs[i] <= kLazyP);  // inf and NaN too
             if (__builtin_expect(__any(cross), 0)) {
 #pragma unroll
                 for (int i = 0; i < SG; ++i) {
-                    const int rb = rb0 + i;
-                    const float mr = max_over_groups(mx[i]);
-                    const bool grow = mr > thr[rb];  // uniform per row
-                    const float m_new = grow ? mr : m_run[rb];
+                    const int rb = j * SG + i;
+                    const float (&sci)[2][4] = sc[j & 1][i];
+                    float ksc[2][4], x[2][4];
+                    score_scale(ksc);
+#pragma unroll
+                    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) x[kt][r] = sci[kt][r] * ksc[kt][r];
+                    const float ml = max_over_groups(vmax(vmax3(x[0][0], x[0][1], x[0][2]),
+                                                          vmax3(x[0][3], x[1][0], x[1][1]),
+                                                          vmax3(x[1][2], x[1][3], x[1][3])));
+                    const bool grow = ml > m_run[rb] + kLazy;  // uniform per row
+                    const float m_new = grow ? ml : m_run[rb];
                     const float alpha = fast_exp2(m_run[rb] - m_new);
                     m_run[rb] = m_new;
-                    thr[rb] = m_new + kLazy;
                     lsum[rb] *= alpha;  // row c: this lane's own
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
@@ -476,110 +520,14 @@ void prefill_dma_kernel(PrefillParams p) {
 #pragma unroll
                         for (int t = 0; t < NT; ++t) o[rb][t][r] *= a;
                     }
+                    if (__any(grow)) p_sum(i, rb, sci);
                 }
             }
-        };
-        // P (fp32) into the row sum; P times the V scale, rounded once,
-        // weights the int8 V values.
-        auto p_group = [&](int rb0, const float (&sc)[SG][2][4], h8 (&pa)[SG]) {
-            float vs[2][4];
-            scales(1, vs);
 #pragma unroll
-            for (int i = 0; i < SG; ++i)
+            for (int i = 0; i < SG; ++i) {
+                lsum[j * SG + i] += bs[i];
 #pragma unroll
-                for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float pr = fast_exp2(sc[i][kt][r] - m_run[rb0 + i]);
-                        lsum[rb0 + i] += pr;
-                        pa[i][4 * kt + r] = (_Float16)(pr * vs[kt][r]);
-                    }
-        };
-        auto pv_group = [&](int rb0, const h8 (&pa)[SG]) {
-#pragma unroll
-            for (int i = 0; i < SG; ++i)
-#pragma unroll
-                for (int t = 0; t < NT; ++t) o[rb0 + i][t] = mfma32(pa[i], vb[t], o[rb0 + i][t]);
-        };
-        if constexpr (SCALED) {
-            // int8: S, max check, exp, P V, one group after the other.
-            float sc[2][SG][2][4], mx[2][SG];
-            h8 pa[SG];
-            s_group(0, sc[0], mx[0]);
-            check_group(0, sc[0], mx[0]);
-#pragma unroll
-            for (int j = 0; j < RB / SG; ++j) {
-                const bool more = j + 1 < RB / SG;
-                const int nx = (j + 1) & 1;
-                p_group(j * SG, sc[j & 1], pa);
-                pv_group(j * SG, pa);
-                if (more) s_group((j + 1) * SG, sc[nx], mx[nx]);
-                if (more) check_group((j + 1) * SG, sc[nx], mx[nx]);
-            }
-        } else {
-            // fp16 P: exp first, check after.  With the running max m, a
-            // score past the lazy threshold (m + kLazy in log2 units) has
-            // P > 2^kLazy, and one far past it overflows fp16 to inf, so the
-            // lane's block sum of P -- which the row sum needs anyway --
-            // exceeds 2^kLazy whenever a row of the lane must be rescaled
-            // (rarely otherwise).  Only then is the row max formed, and the
-            // group's P recomputed if the max moved.  The exp of group j runs
-            // under the S^T MFMAs of group j + 1.
-            float sc[2][SG][2][4];
-            h8 pa[SG];
-            float bs[SG];
-            auto p_sum = [&](int i, int rb, const float (&sci)[2][4]) {
-#pragma unroll
-                for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        pa[i][4 * kt + r] = (_Float16)fast_exp2(fmaf(sci[kt][r], p.scale_log2, -m_run[rb]));
-                float b = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; e += 2)
-                    b = __builtin_amdgcn_fdot2(h2{pa[i][e], pa[i][e + 1]}, h2{1, 1}, b, false);
-                bs[i] = b;
-            };
-            s_group(0, sc[0], nullptr);
-#pragma unroll
-            for (int j = 0; j < RB / SG; ++j) {
-                const bool more = j + 1 < RB / SG;
-                const int nx = (j + 1) & 1;
-#pragma unroll
-                for (int i = 0; i < SG; ++i) p_sum(i, j * SG + i, sc[j & 1][i]);
-                if (more) s_group((j + 1) * SG, sc[nx], nullptr);
-                bool cross = false;
-#pragma unroll
-                for (int i = 0; i < SG; ++i) cross |= !(bs[i] <= kLazyP);  // inf and NaN too
-                if (__builtin_expect(__any(cross), 0)) {
-#pragma unroll
-                    for (int i = 0; i < SG; ++i) {
-                        const int rb = j * SG + i;
-                        const float (&sci)[2][4] = sc[j & 1][i];
-                        const float mr = max_over_groups(vmax(vmax3(sci[0][0], sci[0][1], sci[0][2]),
-                                                              vmax3(sci[0][3], sci[1][0], sci[1][1]),
-                                                              vmax3(sci[1][2], sci[1][3], sci[1][3])));
-                        const float ml = mr * p.scale_log2;
-                        const bool grow = ml > m_run[rb] + kLazy;  // uniform per row
-                        const float m_new = grow ? ml : m_run[rb];
-                        const float alpha = fast_exp2(m_run[rb] - m_new);
-                        m_run[rb] = m_new;
-                        lsum[rb] *= alpha;  // row c: this lane's own
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const float a = shfl(alpha, 4 * g + r);
-#pragma unroll
-                            for (int t = 0; t < NT; ++t) o[rb][t][r] *= a;
-                        }
-                        if (__any(grow)) p_sum(i, rb, sci);
-                    }
-                }
-#pragma unroll
-                for (int i = 0; i < SG; ++i) {
-                    lsum[j * SG + i] += bs[i];
-#pragma unroll
-                    for (int t = 0; t < NT; ++t) o[j * SG + i][t] = mfma32(pa[i], vb[t], o[j * SG + i][t]);
-                }
+                for (int t = 0; t < NT; ++t) o[j * SG + i][t] = mfma32(pa[i], vb[t], o[j * SG + i][t]);
             }
         }
     };
