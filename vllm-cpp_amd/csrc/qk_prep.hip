@@ -22,6 +22,7 @@
 // per (batch row, d) with d in the first half of its head, cos/sin indexed by
 // the pair, the partner index clamped to d past total_dim as the reference does.
 #include "qk_prep.h"
+#include "device_common.h"
 
 #pragma clang fp contract(off)
 
@@ -144,6 +145,120 @@ __global__ __launch_bounds__(kQkWaves * 64) void qk_prep_kernel(QkPrepParams p) 
     }
 }
 
+// The same work for head_dim 64, 80 or 128 with 16-byte aligned rows, staged
+// through LDS.  A wave's rows are one contiguous run of nrows * D floats: it
+// moves in and out with fully coalesced 16-byte lane accesses.  Between the
+// two, lane (row lane / 4, quarter lane % 4) owns the D / 4 consecutive
+// elements of that quarter of the row, so
+//  - the row's sum of squares is a two-step quad reduction (DPP),
+//  - interleaved pairs (2i, 2i + 1) lie inside a lane, and the half-split
+//    partner e +- D / 2 is the same slot of quarter q ^ 2 (a DPP quad swap),
+//  - cos/sin of the token's D / 2 pair angles are formed once per wave into a
+//    table beside the tile.
+// Arithmetic per element is the generic kernel's, statement by statement.
+template <int D>
+__global__ __launch_bounds__(kQkWaves * 64) void qk_prep_lds_kernel(QkPrepParams p) {
+    constexpr int P = D / 2, EQ = D / 4;          // pairs; elements per lane
+    constexpr int NQ = kRows * D / 4;             // 16-byte units of a full tile
+    constexpr int NK = (NQ + 63) / 64;            // per lane
+    static_assert(EQ % 4 == 0, "a lane's quarter is whole 16-byte units");
+    __shared__ __attribute__((aligned(16))) float tile_all[kQkWaves][kRows * D];
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    __shared__ f2 cs_all[kQkWaves][P];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t item = (int64_t)blockIdx.x * kQkWaves + __builtin_amdgcn_readfirstlane(wave);
+    const int gq = (p.t[0].num_heads + kRows - 1) / kRows;
+    const int gk = p.t[1].x ? (p.t[1].num_heads + kRows - 1) / kRows : 0;
+    const int64_t tok = item / (gq + gk);
+    if (tok >= p.num_tokens) return;
+    const int grp = (int)(item - tok * (gq + gk));
+    const int which = grp >= gq;
+    const QkTensor T = p.t[which];
+    const int h0 = (which ? grp - gq : grp) * kRows;
+    const int nrows = min(kRows, T.num_heads - h0);
+    const int nq = nrows * (D / 4);
+    const bool half = p.style == VCPP_ROPE_HALF;
+    const bool rot = p.positions != nullptr;
+    const bool norm = T.norm_weight != nullptr;
+    f4* base = reinterpret_cast<f4*>(T.x + (tok * T.num_heads + h0) * D);
+    auto* tile = (__attribute__((address_space(3))) float*)(tile_all[wave]);
+    auto* cs = (__attribute__((address_space(3))) f2*)(cs_all[wave]);
+
+    f4 in[NK];
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+        const int idx = 64 * k + lane;
+        in[k] = base[min(idx, nq - 1)];  // past the rows: a valid unit, not stored
+    }
+    if (rot && lane < P) {
+        float sn, c;
+        sincosf(p.inv_freq[min(lane, p.inv_freq_size - 1)] * (float)p.positions[tok], &sn, &c);
+        cs[lane] = f2{c, sn};
+    }
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+        const int idx = 64 * k + lane;
+        if (idx < NQ) reinterpret_cast<__attribute__((address_space(3))) f4*>(tile)[idx] = in[k];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    const int r = lane >> 2, qq = lane & 3, e0 = qq * EQ;
+    __attribute__((address_space(3))) float* row = tile + r * D + e0;
+    float x[EQ];
+#pragma unroll
+    for (int m = 0; m < EQ / 4; ++m) {
+        const f4 v = reinterpret_cast<__attribute__((address_space(3))) f4*>(row)[m];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[4 * m + i] = v[i];
+    }
+    float inv = 1.f;
+    if (norm) {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < EQ; ++i) ss += x[i] * x[i];
+        ss += dpp<0xB1>(ss);  // quad_perm [1,0,3,2]
+        ss += dpp<0x4E>(ss);  // quad_perm [2,3,0,1]
+        inv = __builtin_amdgcn_rcpf(__builtin_amdgcn_sqrtf(ss * (1.0f / (float)D) + p.eps));
+    }
+    float y[EQ];
+#pragma unroll
+    for (int i = 0; i < EQ; ++i) y[i] = norm ? T.norm_weight[e0 + i] * x[i] * inv : x[i];
+    if (rot) {
+        if (half) {
+            // partner of e (quarter qq) is e +- P: the same slot of quarter qq ^ 2
+            const bool lo = qq < 2;
+#pragma unroll
+            for (int i = 0; i < EQ; ++i) {
+                const float yp = dpp<0x4E>(y[i]);
+                const f2 t = cs[lo ? e0 + i : e0 + i - P];
+                y[i] = lo ? y[i] * t.x - yp * t.y : yp * t.y + y[i] * t.x;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < EQ; i += 2) {
+                const f2 t = cs[(e0 + i) >> 1];
+                const float a = y[i], b = y[i + 1];
+                y[i] = a * t.x - b * t.y;      // x0 c - x1 s
+                y[i + 1] = a * t.y + b * t.x;  // x0 s + x1 c
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < EQ / 4; ++m)
+        reinterpret_cast<__attribute__((address_space(3))) f4*>(row)[m] =
+            f4{y[4 * m], y[4 * m + 1], y[4 * m + 2], y[4 * m + 3]};
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+        const int idx = 64 * k + lane;
+        if (idx < nq) base[idx] = reinterpret_cast<__attribute__((address_space(3))) f4*>(tile)[idx];
+    }
+}
+
 __global__ __launch_bounds__(256) void rope_table_kernel(RopeTableParams p) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= (int64_t)p.batch_size * p.total_dim) return;
@@ -172,7 +287,12 @@ hipError_t launch_qk_prep(const QkPrepParams& p, hipStream_t stream) {
                            (p.t[1].x ? (p.t[1].num_heads + kRows - 1) / kRows : 0);
     const int64_t wg = ((int64_t)p.num_tokens * groups + kQkWaves - 1) / kQkWaves;
     const dim3 grid((unsigned)wg), block(kQkWaves * 64);
-    if (p.head_dim <= 64) hipLaunchKernelGGL(qk_prep_kernel<1>, grid, block, 0, stream, p);
+    const bool aligned = reinterpret_cast<uintptr_t>(p.t[0].x) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(p.t[1].x) % 16 == 0;
+    if (aligned && p.head_dim == 80) hipLaunchKernelGGL(qk_prep_lds_kernel<80>, grid, block, 0, stream, p);
+    else if (aligned && p.head_dim == 64) hipLaunchKernelGGL(qk_prep_lds_kernel<64>, grid, block, 0, stream, p);
+    else if (aligned && p.head_dim == 128) hipLaunchKernelGGL(qk_prep_lds_kernel<128>, grid, block, 0, stream, p);
+    else if (p.head_dim <= 64) hipLaunchKernelGGL(qk_prep_kernel<1>, grid, block, 0, stream, p);
     else if (p.head_dim <= 128) hipLaunchKernelGGL(qk_prep_kernel<2>, grid, block, 0, stream, p);
     else hipLaunchKernelGGL(qk_prep_kernel<4>, grid, block, 0, stream, p);
     return hipGetLastError();
