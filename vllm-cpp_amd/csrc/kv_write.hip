@@ -171,7 +171,19 @@ __global__ __launch_bounds__(256) void kv_write_vec_kernel(KvWriteParams p, int 
         } else {
             float amax = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
             float row_max = amax;
-            for (int j = 0; j < L; ++j) row_max = fmaxf(row_max, __shfl(amax, seg * L + j, 64));
+            if (L % 4 == 0) {
+                // Segments of whole quads (a row's lanes all active or all
+                // returned): the quad's max by two DPP quad permutes, then one
+                // read per quad of the segment (max is exact in any order).
+                float qm = fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                           0, __builtin_bit_cast(int, amax), 0xB1, 0xF, 0xF, false)));
+                qm = fmaxf(qm, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                   0, __builtin_bit_cast(int, qm), 0x4E, 0xF, 0xF, false)));
+                row_max = qm;
+                for (int j = 0; j < L; j += 4) row_max = fmaxf(row_max, __shfl(qm, seg * L + j, 64));
+            } else {
+                for (int j = 0; j < L; ++j) row_max = fmaxf(row_max, __shfl(amax, seg * L + j, 64));
+            }
             const uint16_t sh = f16_rne(row_max / 127.0f);
             const float sc = f16_to_f32(sh);
             const float xs[4] = {x.x, x.y, x.z, x.w};
