@@ -6,10 +6,24 @@
 // The reference's GPU slot is cuda/attention.cu:11-52; its kernel
 // (cuda/attention_kernels.cuh:9-123) is not followed.
 //
-// fp16 / int8 pages (the HBM-bound path):
-//  * One wave per (kv head, chunk of <= 8 query heads of its GQA group): every
-//    K/V page is read from HBM once for the whole group.  Workgroups hold 4
-//    waves = 4 kv heads = 640 contiguous bytes of each token row.
+// fp16 / int8 / FP8 pages (the HBM-bound path) run one of two kernels with the
+// same split, MFMA step and merge (below).
+//  * decode_page_kernel -- Hkv = 8, <= 8 query heads per kv head, D 64 or 80,
+//    balanced split: a workgroup of 8 waves (one per kv head) walks its range
+//    of 16-token tiles.  Each tile's K rows and V rows (16 tokens x all kv
+//    heads: one contiguous run of the page each) are DMA'd into an LDS ring
+//    with global_load_lds_dwordx4 (1 KiB of whole lines per instruction,
+//    explicit vmcnt bookkeeping), chunk order XOR-swizzled by token, one
+//    barrier per tile.  fp16: a 3-tile ring, one workgroup per CU.  Byte
+//    pages: a 3-tile ring per workgroup and two workgroups per CU; K widened
+//    in registers, V read transposed straight from the byte tile with
+//    ds_read_b64_tr_b8, int8 scales in one more DMA instruction per tile.
+//  * decode_mfma_kernel -- every other shape, and fixed partitions: one wave
+//    per (kv head, chunk of <= 8 query heads of its GQA group); workgroups hold
+//    4 waves = 4 kv heads = 640 contiguous bytes of each token row.  Its loads
+//    are described at the end of this comment.
+// Both kernels:
+//  * Every K/V page is read from HBM once for a kv head's whole GQA group.
 //  * Balanced split: the 16-token tiles of all sequences are laid end to end
 //    and every resident workgroup takes an equal contiguous range of them, so
 //    ragged batches keep the whole GPU busy to the end.  A range touches 1-3
@@ -19,14 +33,15 @@
 //    partials that a log-sum-exp merge kernel combines.
 //  * A 16-token tile is one MFMA step:
 //      S^T[16 tok][16] = K_tile[16 tok][D] x Qs^T   (16x16x32 f16; a 16-dim
-//                                                    remainder as 16x16x16)
+//                                                    remainder as 16x16x16 into
+//                                                    its own accumulator)
 //      O[16][D]       += P[16][16 tok] x V_tile      (16x16x16 f16)
 //    The 16 MFMA rows hold the fp16 "hi" part of the 8 query heads (rows 0-7)
 //    and the fp16 residual q - hi (rows 8-15); likewise P = p_hi + p_lo, so
 //    q and p keep about 22 significant bits while K/V stay exact fp16, with
 //    fp32 accumulation: the rows an 8-head group would waste carry the low
 //    halves instead.
-//  * K fragments come straight from HBM into registers (one 16-byte buffer
+//  * decode_mfma_kernel: K fragments come straight from HBM into registers (one 16-byte buffer
 //    load per lane per 32 dims).  V is staged row-major in LDS and read back
 //    with ds_read_b64_tr_b16, which hands each lane four tokens of one dim --
 //    the P x V operand -- in one instruction.
@@ -1204,12 +1219,15 @@ void decode_page_kernel(DecodeParams p) {
 template <int KV, int D>
 hipError_t launch_page(const DecodeParams& p, hipStream_t stream) {
     const size_t lds = PageCfg<KV, D>::LDS;
-    static bool attr_set = false;  // one device per process
-    if (!attr_set) {
+    // The LDS limit is a per-device property of the kernel: set it once on
+    // each device the library launches on (idempotent if two threads race).
+    static bool attr_set[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || !attr_set[dev]) {
         const hipError_t e = hipFuncSetAttribute((const void*)decode_page_kernel<KV, D>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
-        attr_set = true;
+        if (dev >= 0 && dev < 64) attr_set[dev] = true;
     }
     hipLaunchKernelGGL((decode_page_kernel<KV, D>), dim3(p.num_wg), dim3(kPageWaves * 64), lds, stream, p);
     return hipGetLastError();

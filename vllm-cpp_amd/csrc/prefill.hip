@@ -11,23 +11,30 @@
 //
 // Work decomposition: a workgroup = (16*RB-token query tile, chunk, kv head,
 // group of 4 query heads); one wave per query head holds RB row blocks of 16
-// query tokens.  Keys stream in blocks of 32 (two 16-token tiles) through
-// double-buffered LDS: the workgroup gathers each block's K and V rows of its
-// kv head through the block table with 16-byte loads (int8 pages are
-// dequantised to fp16 here).  Per row block and key block:
-//   S^T[32 keys][16 rows] = K_blk x Q^T    (16x16x32 f16; a 16-dim remainder
-//                                           as 16x16x16 into its own accumulator)
-//   O[16 rows][D | 16]  += P x [V_blk | 1] (16x16x32 f16, P straight from the
-//                                           S^T accumulator layout)
-// The all-ones extra column block yields the row sums of exactly the fp16 P
-// that multiplies V.  The running max is only moved (and O rescaled) when a
-// row's max grows by more than 2^8, so P stays <= 256 and most blocks skip
-// the rescale.  Causal masks are applied only on key blocks that reach past
-// the first query token of the tile.
+// query tokens.  Keys stream in blocks of 32 through a ring of LDS stages that
+// the workgroup fills with direct-to-LDS DMA (global_load_lds_dwordx4, one
+// page lookup per lane, explicit vmcnt bookkeeping), two blocks per barrier.
+// Byte pages (int8, FP8) arrive raw and are widened by the workgroup into an
+// fp16 area: FP8 to its values, int8 K to exact integers (its per-key scale
+// joins the exp's fma below) and int8 V to fp16(v * scale).  Per row block
+// and key block:
+//   S^T[32 keys][16 rows] = K_blk x Q^T   (16x16x32 f16; at D = 80 the 16-dim
+//                                          remainder reads an LDS zero slot in
+//                                          the upper k half)
+//   P = exp2(fma(S, scale, -m)) as fp16   (scale = log2(e)/sqrt(D), times the
+//                                          key's scale on int8 pages)
+//   O[16 rows][D]        += P x V_blk     (16x16x32 f16, P straight from the
+//                                          S^T accumulator layout)
+// Row sums are v_dot2 sums of exactly the fp16 P that multiplies V.  The
+// running max moves lazily: only when a row's max grows by more than 2^8,
+// detected after the exp from the lane's block sum of P (so most blocks form
+// no max at all).  Causal masks are applied only on key blocks that reach
+// past the first query token of the tile.
 #include "device_common.h"
 #include "prefill.h"
 #include "profile.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace vcpp {
@@ -600,14 +607,17 @@ hipError_t launch_dma(const PrefillParams& p, hipStream_t stream) {
     dim3 grid((p.max_chunk_len + QT - 1) / QT, p.num_chunks,
               p.num_kv_heads * p.head_groups);
     const size_t lds = prefill_lds_bytes(KV, D, p.max_blocks);
-    // Raise the kernel's dynamic LDS limit only when a launch needs more than
-    // it was last set to (the attribute call is a host round trip).
-    static size_t attr_lds = 65536;  // one device per process
-    if (lds > attr_lds) {
+    // Raise the kernel's dynamic LDS limit on this device only when a launch
+    // needs more than it was last set to there (the attribute call is a host
+    // round trip; the limit is per device).
+    static size_t attr_lds[64] = {};
+    int dev = 0;
+    const bool known = hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64;
+    if (!known || lds > std::max<size_t>(attr_lds[dev], 65536)) {
         const hipError_t e = hipFuncSetAttribute((const void*)prefill_dma_kernel<KV, D>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
-        attr_lds = lds;
+        if (known) attr_lds[dev] = lds;
     }
     hipLaunchKernelGGL((prefill_dma_kernel<KV, D>), grid, dim3(256), lds, stream, p);
     return hipGetLastError();
