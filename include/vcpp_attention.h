@@ -141,7 +141,9 @@ size_t vcpp_decode_workspace_size(const vcpp_kv_pages* kv, int32_t num_seqs, int
  *   prefix_lens  [num_chunks] int32 on the device
  *   max_chunk_len host-side upper bound of the chunk lengths (sizes the grid)
  * KV dtypes: VCPP_KV_F16, VCPP_KV_I8 and VCPP_KV_FP8 (byte pages are widened to fp16 on the
- * way into LDS); head_dim 64, 80 or 128; num_heads / num_kv_heads any.
+ * way into LDS: FP8 to its values; int8 K to exact integers whose per-key scale multiplies the
+ * score in fp32, int8 V to fp16(v * scale), one rounding); head_dim 64, 80 or 128;
+ * num_heads / num_kv_heads any.
  * Replaces read_kv_prefill + compute_attention per position
  * (src/paged_attention.cpp:174-201, src/paged_engine.cpp:64-113,381-384).
  */
