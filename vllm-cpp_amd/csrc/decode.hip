@@ -974,24 +974,45 @@ void decode_page_kernel(DecodeParams p) {
         }
         const bool complete = first_tis == 0 && last_tis == cur_ntiles - 1;
         const int slot = first_tis == 0 ? 1 : 0;
-        if (g < 2) {
+        // Rows 4 (g & 1) + r hold head rows; after the half-wave sum every
+        // lane has its row's values, so all lanes store: pass k takes register
+        // r = k + 2 (g >> 1), even lanes store pass 0 and odd lanes pass 1 as
+        // column pairs (the pair's other value one DPP swap away).  One float2
+        // store per 16 columns keeps the finalize off the memory queue that
+        // the DMA ring fills.
+        const int rk0 = 2 * (g >> 1), rk1 = rk0 + 1;
+        const bool odd = (c & 1) != 0;
+        const int rr = odd ? rk1 : rk0;
+        const int h = 4 * (g & 1) + rr;
+        const int64_t blk = ((int64_t)w * 2 + slot) * p.pairs + pair;
+        float* orow = complete ? p.out + ((int64_t)cur * p.num_heads + head_base + h) * D
+                               : p.ws_o + (blk * 8 + h) * D;
+        float lsel = lh[0];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int h = 4 * g + r;
-                if (h >= gc) continue;
-                if (complete) {
-                    const float inv = 1.0f / (lh[r] + 1e-9f);
-                    float* orow = p.out + ((int64_t)cur * p.num_heads + head_base + h) * D;
+        for (int r = 1; r < 4; ++r) lsel = rr == r ? lh[r] : lsel;
+        const float scl = complete ? 1.0f / (lsel + 1e-9f) : 1.0f;
+        if (h < gc) {
 #pragma unroll
-                    for (int t = 0; t < NT; ++t) orow[16 * t + c] = o[t][r] * inv;
-                } else {
-                    const int64_t blk = ((int64_t)w * 2 + slot) * p.pairs + pair;
-                    float* orow = p.ws_o + (blk * 8 + h) * D;
-#pragma unroll
-                    for (int t = 0; t < NT; ++t) orow[16 * t + c] = o[t][r];
-                    if (c == 0) p.ws_ml[blk * 16 + h] = make_float2(mh[r], lh[r]);
+            for (int t = 0; t < NT; ++t) {
+                float x0 = o[t][0], x1 = o[t][1];
+                if (rk0 == 2) {
+                    x0 = o[t][2];
+                    x1 = o[t][3];
                 }
+                const float y = dpp_swap1(odd ? x0 : x1);  // neighbour in the pair
+                const float2 v = odd ? make_float2(y * scl, x1 * scl) : make_float2(x0 * scl, y * scl);
+                *reinterpret_cast<float2*>(orow + 16 * t + (c & ~1)) = v;
             }
+        }
+        // (m, l) of the partial: lanes c < 4 of the first two groups, row 4 g + c
+        if (!complete && g < 2 && c < 4 && 4 * g + c < gc) {
+            float ms = mh[0], ls = lh[0];
+#pragma unroll
+            for (int r = 1; r < 4; ++r) {
+                ms = c == r ? mh[r] : ms;
+                ls = c == r ? lh[r] : ls;
+            }
+            p.ws_ml[blk * 16 + 4 * g + c] = make_float2(ms, ls);
         }
     };
 

@@ -35,6 +35,11 @@ __device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
+// Value of lane l ^ 1 (DPP quad_perm [1,0,3,2]).
+__device__ __forceinline__ float dpp_swap1(float x) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false));
+}
+
 // Value of lane (l ^ 8) within each 16-lane row (DPP row_ror:8).
 __device__ __forceinline__ float dpp_ror8(float x) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xF, 0xF, false));
