@@ -47,6 +47,10 @@ constexpr int32_t kMaxPartition = 1024;
 // fp16/int8 split: at least one 64-token step per range; grid.x limit.
 constexpr int64_t kMinTilesPerRange = 4;
 constexpr int64_t kMaxRanges = 1 << 20;
+// Page-staged decode: the balanced split charges each sequence this many
+// 16-token tiles for starting it (its Q load, the previous one's outputs).  A
+// sweep of 0, 2, 4, 6, 8 on BASELINE config 2 put the step's best at 2.
+constexpr int kSwitchTiles = 2;
 
 int32_t ceil_div(int64_t a, int64_t b) { return (int32_t)((a + b - 1) / b); }
 
@@ -323,6 +327,7 @@ int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
     p.max_parts = pl.max_parts;
     p.num_wg = pl.num_wg;
     p.page_mode = pl.page_mode ? 1 : 0;
+    p.switch_tiles = pl.page_mode ? kSwitchTiles : 0;
     p.ctx_cap = max_context_len;
     if (need > 0) {
         p.ws_o = reinterpret_cast<float*>(ws + pl.off_o);

@@ -38,6 +38,10 @@ struct DecodeParams {
     // fp16/int8: balanced split of the concatenated 16-token tiles over
     // num_wg workgroup ranges (per kv-head group)
     int32_t num_wg;
+    // Cost of starting a sequence in a range, in tiles: the split divides
+    // T + switch_tiles * (non-empty sequences) evenly, each sequence's tiles
+    // preceded by switch_tiles units that hold no tile (0: plain tile split).
+    int32_t switch_tiles;
     int32_t ctx_cap;       // context lengths are clamped to this
     // fp32: fixed partitions of `partition` tokens, max_parts per sequence
     int32_t partition;

@@ -641,20 +641,24 @@ __global__ __launch_bounds__(256) void merge_split_kernel(DecodeParams p) {
     const int pair = blockIdx.y * 4 + wave;
     const int s = blockIdx.x;
     if (pair >= p.pairs) return;
-    const int G = p.num_wg;
-    int T = 0, S = 0;
+    const int G = p.num_wg, X = p.switch_tiles;
+    int T = 0, S = 0, K = 0, KS = 0;  // tiles and non-empty sequences: all, before s
     for (int base = 0; base < p.num_seqs; base += 64) {
         const int sl = base + lane;
         const int nt = sl < p.num_seqs ? tiles_of(p, sl) : 0;
         T += wave_sum(nt);
         S += wave_sum(sl < s ? nt : 0);
+        K += wave_sum(nt > 0 ? 1 : 0);
+        KS += wave_sum(sl < s && nt > 0 ? 1 : 0);
     }
     const int E = S + tiles_of(p, s);
     if (E <= S) return;  // no tiles: zeroed by the decode kernel
-    const int w0 = range_of(S, T, G), w1 = range_of(E - 1, T, G);
+    // the split's axis: tile t of s sits at t + X (non-empty sequences up to s)
+    const int Tv = T + X * K, shift = X * (KS + 1);
+    const int w0 = range_of(S + shift, Tv, G), w1 = range_of(E - 1 + shift, Tv, G);
     if (w0 == w1) return;  // finished in place
     const int kvh = pair / p.qchunks, qc = pair - kvh * p.qchunks;
-    merge_fragments<D>(p, s, w0, w1, pair, kvh * p.group + qc * 8, min(8, p.group - qc * 8), T,
+    merge_fragments<D>(p, s, w0, w1, pair, kvh * p.group + qc * 8, min(8, p.group - qc * 8), Tv,
                        lane, reinterpret_cast<__attribute__((address_space(3))) float*>(
                                  (__attribute__((address_space(3))) float*)wts_all[wave]));
 }
@@ -887,10 +891,40 @@ void decode_page_kernel(DecodeParams p) {
     const int head_base = kvh * p.group;
     const int gc = p.group;
 
-    int T = 0;
-    for (int base = 0; base < p.num_seqs; base += 64)
-        T += wave_sum(base + lane < p.num_seqs ? tiles_of(p, base + lane) : 0);
-    const int a = range_start(w, T, G), b = range_start(w + 1, T, G);
+    // The split: ranges divide T + X K evenly, where sequence j's tiles are
+    // preceded by X units that hold no tile (the cost of starting it), and
+    // each range's bounds map back to real tile indices a, b.
+    const int X = p.switch_tiles;
+    int T = 0, K = 0;
+    for (int base = 0; base < p.num_seqs; base += 64) {
+        const int nt = base + lane < p.num_seqs ? tiles_of(p, base + lane) : 0;
+        T += wave_sum(nt);
+        K += wave_sum(nt > 0 ? 1 : 0);
+    }
+    const int Tv = T + X * K;
+    // first real tile at or past virtual position V
+    auto real_of = [&](int V) -> int {
+        if (X == 0 || V <= 0) return max(V, 0);
+        if (V >= Tv) return T;
+        int cs = 0, ck = 0;
+        for (int base = 0; base < p.num_seqs; base += 64) {
+            const int sl = base + lane;
+            const int nt = sl < p.num_seqs ? tiles_of(p, sl) : 0;
+            const int Sl = cs + wave_excl_scan(nt, lane);
+            const int kl = ck + wave_excl_scan(nt > 0 ? 1 : 0, lane);
+            const int vfirst = Sl + X * (kl + 1);  // virtual position of its first tile
+            const uint64_t hit = __ballot(nt > 0 && V >= vfirst - X && V < vfirst + nt);
+            if (hit) {
+                const int j = __builtin_ctzll(hit);
+                const int Sj = __builtin_amdgcn_readlane(Sl, j), kj = __builtin_amdgcn_readlane(kl, j);
+                return max(Sj, V - X * (kj + 1));
+            }
+            cs += wave_sum(nt);
+            ck += wave_sum(nt > 0 ? 1 : 0);
+        }
+        return T;
+    };
+    const int a = real_of(range_start(w, Tv, G)), b = real_of(range_start(w + 1, Tv, G));
     const bool zero_owner_tail = (T == 0 && w == 0) || (T > 0 && w == G - 1);
 
     // Zero the outputs of empty sequences this range owns (wave 0).
