@@ -183,19 +183,23 @@ def test_workspace_reuse(cuda, partition):
         assert_close(out.cpu().numpy(), want, *TOL[O.ORC_F16], what="reuse it=%d" % it)
 
 
-def test_many_short_sequences(cuda):
+@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8, O.ORC_FP8])
+def test_many_short_sequences(cuda, kind):
     """Hundreds of short, ragged sequences (many per workgroup range, several
-    empty): the balanced split switches sequence inside ranges constantly."""
+    empty) and a few long ones that span several ranges: the balanced split
+    (which charges every sequence start) switches sequence inside ranges
+    constantly, over several 64-sequence scan steps."""
     rng = np.random.default_rng(3)
     ctx = rng.integers(0, 70, 700).astype(np.int32)
     ctx[::37] = 0
+    ctx[[5, 300, 301, 650]] = [3000, 2500, 40, 4096]
     nb = int(sum((c + 15) // 16 for c in ctx)) + 16
-    pool = O.make_pool(O.ORC_F16, 211, nb, 8, 80)
+    pool = O.make_pool(kind, 211, nb, 8, 80)
     q = O.normal(212, (len(ctx), 64, 80))
     tables = random_tables(213, ctx, nb)
     want = O.decode(pool, q, tables, ctx, 64)
     got = gpu_decode(DevPool(pool), q, tables, ctx, 64)
-    assert_close(got, want, *TOL[O.ORC_F16], what="many short")
+    assert_close(got, want, *TOL[kind], what="many short kind=%d" % kind)
     assert np.all(got[ctx == 0] == 0.0)
 
 
