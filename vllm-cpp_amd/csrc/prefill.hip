@@ -69,8 +69,6 @@ __device__ __forceinline__ h4 read_tr(lds_char* a) {
     return __builtin_bit_cast(h4, x);
 }
 
-__device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
-
 // ---------------------------------------------------------------------------
 // fp16 pages: direct-to-LDS gathers through a ring of kStages key blocks.
 //
