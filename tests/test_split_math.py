@@ -1,0 +1,106 @@
+"""The decode split's integer arithmetic, restated from the two kernels that
+must agree on it, checked for consistency on random and edge-case batches.
+
+decode_page_kernel (vllm-cpp_amd/csrc/decode.hip) gives range w the real
+tiles [real_of(range_start(w, Tv, G)), real_of(range_start(w + 1, Tv, G))),
+where the split axis puts X units before each non-empty sequence's tiles
+(Tv = T + X K).  merge_split_kernel maps a sequence's first and last tiles to
+ranges with range_of(t + X (k + 1), Tv, G).  If the two disagreed, a partial
+would be written to one range's slot and read from another's; these checks
+pin that they cannot."""
+import numpy as np
+import pytest
+
+
+def range_start(w, T, G):
+    return (w * T) // G
+
+
+def range_of(t, T, G):
+    return ((t + 1) * G - 1) // T
+
+
+def range_live(w, T, G):
+    return T >= G or range_start(w, T, G) < range_start(w + 1, T, G)
+
+
+def axis(tiles, X):
+    """Real prefix S, non-empty count before each sequence k, totals."""
+    S = np.concatenate([[0], np.cumsum(tiles)])[:-1]
+    k = np.concatenate([[0], np.cumsum(tiles > 0)])[:-1]
+    return S, k, int(tiles.sum()), int((tiles > 0).sum())
+
+
+def real_of(V, tiles, X):
+    """decode_page_kernel's real_of: first real tile at or past virtual V."""
+    S, k, T, K = axis(tiles, X)
+    Tv = T + X * K
+    if X == 0 or V <= 0:
+        return max(V, 0)
+    if V >= Tv:
+        return T
+    for s in range(len(tiles)):
+        nt = int(tiles[s])
+        vfirst = int(S[s]) + X * (int(k[s]) + 1)
+        if nt > 0 and vfirst - X <= V < vfirst + nt:
+            return max(int(S[s]), V - X * (int(k[s]) + 1))
+    return T
+
+
+def ranges(tiles, X, G):
+    S, k, T, K = axis(tiles, X)
+    Tv = T + X * K
+    return [(real_of(range_start(w, Tv, G), tiles, X), real_of(range_start(w + 1, Tv, G), tiles, X))
+            for w in range(G)], T, Tv
+
+
+def check(tiles, X, G):
+    tiles = np.asarray(tiles, dtype=np.int64)
+    rs, T, Tv = ranges(tiles, X, G)
+    # contiguous, in order, covering [0, T) (ranges may be empty when Tv < G)
+    assert rs[0][0] == 0 and rs[-1][1] == T
+    for (a0, b0), (a1, b1) in zip(rs, rs[1:]):
+        assert a0 <= b0 == a1 <= b1
+    owner = np.empty(T, dtype=np.int64)
+    for w, (a, b) in enumerate(rs):
+        owner[a:b] = w
+    # the merge kernel's view of every sequence's first and last tiles
+    S, k, _, _ = axis(tiles, X)
+    for s, nt in enumerate(tiles):
+        if nt == 0:
+            continue
+        shift = X * (int(k[s]) + 1)
+        first, last = int(S[s]), int(S[s]) + int(nt) - 1
+        assert range_of(first + shift, Tv, G) == owner[first]
+        assert range_of(last + shift, Tv, G) == owner[last]
+        # the merge reads the ranges between that range_live calls live: those
+        # hold tiles of s, the others hold none
+        for w in range(owner[first], owner[last] + 1):
+            a, b = rs[w]
+            if range_live(w, Tv, G):
+                assert a < b and a <= last and b > first
+            else:
+                assert a == b
+
+
+@pytest.mark.parametrize("X", [0, 1, 2, 4, 7])
+def test_split_random_batches(X):
+    rng = np.random.default_rng(1234 + X)
+    for _ in range(60):
+        n = int(rng.integers(1, 200))
+        tiles = rng.integers(0, 300, n)
+        tiles[rng.random(n) < 0.2] = 0  # empty sequences
+        G = int(rng.choice([1, 3, 64, 256, 512]))
+        if tiles.sum() == 0:
+            tiles[0] = 1
+        check(tiles, X, G)
+
+
+@pytest.mark.parametrize("X", [0, 2])
+def test_split_edge_cases(X):
+    check([1], X, 256)                      # far fewer tiles than ranges
+    check([0, 0, 5, 0], X, 7)               # empty sequences around one short one
+    check([256] * 64, X, 256)               # BASELINE config 2's shape class
+    check([2048] * 16, X, 256)              # config 4's shape class
+    check([1] * 1000, X, 256)               # many one-tile sequences
+    check([3000, 1, 1, 1, 4096], X, 512)    # long ones around short ones
