@@ -1050,35 +1050,60 @@ void decode_page_kernel(DecodeParams p) {
         }
     };
 
-    auto start_seq = [&](const PageEntry& e) {
-        cur = e.seq;
-        first_tis = e.tis;
-        cur_ntiles = e.ntiles;
-        cur_end = e.end;
+    // Raw q rows of this wave's heads for sequence `seq` (lane (g, c): head
+    // c & 7, dims 32 cc + 8 g .. + 7 and the remainder's 4 g .. + 3), and
+    // their hi/lo fp16 split into the MFMA operands.
+    constexpr int QN = 2 * NC32 + (Dims<D>::REM ? 1 : 0);
+    auto load_q = [&](int seq, f4 (&xq)[QN]) {
         const bool qv = (c & 7) < gc;
-        const float* qrow = p.q + ((int64_t)cur * p.num_heads + head_base + (c & 7)) * D;
+        const float* qrow = p.q + ((int64_t)seq * p.num_heads + head_base + (c & 7)) * D;
 #pragma unroll
         for (int cc = 0; cc < NC32; ++cc) {
-            f4 x0 = {}, x1 = {};
-            if (qv) {
-                x0 = *reinterpret_cast<const f4*>(qrow + 32 * cc + 8 * g);
-                x1 = *reinterpret_cast<const f4*>(qrow + 32 * cc + 8 * g + 4);
-            }
+            xq[2 * cc] = qv ? *reinterpret_cast<const f4*>(qrow + 32 * cc + 8 * g) : f4{};
+            xq[2 * cc + 1] = qv ? *reinterpret_cast<const f4*>(qrow + 32 * cc + 8 * g + 4) : f4{};
+        }
+        if constexpr (Dims<D>::REM)
+            xq[2 * NC32] = qv ? *reinterpret_cast<const f4*>(qrow + 32 * NC32 + 4 * g) : f4{};
+    };
+    auto split_q = [&](const f4 (&xq)[QN]) {
+#pragma unroll
+        for (int cc = 0; cc < NC32; ++cc) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const float x = i < 4 ? x0[i] : x1[i - 4];
+                const float x = i < 4 ? xq[2 * cc][i] : xq[2 * cc + 1][i - 4];
                 const _Float16 hi = (_Float16)x;
                 qa[cc][i] = c < 8 ? hi : (_Float16)(x - (float)hi);
             }
         }
         if constexpr (Dims<D>::REM) {
-            f4 x = {};
-            if (qv) x = *reinterpret_cast<const f4*>(qrow + 32 * NC32 + 4 * g);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const _Float16 hi = (_Float16)x[i];
-                qr[i] = c < 8 ? hi : (_Float16)(x[i] - (float)hi);
+                const float x = xq[2 * NC32][i];
+                const _Float16 hi = (_Float16)x;
+                qr[i] = c < 8 ? hi : (_Float16)(x - (float)hi);
             }
+        }
+    };
+    // fp16 pages: q of the sequence holding the range's first tile is loaded
+    // with the tile list (its wait is the list's), so the first tile does not
+    // wait for the DMA ring the way a later start_seq's load does.  (Byte
+    // pages run 4 waves per SIMD and have no registers for it.)
+    constexpr bool PRE_Q = !BYTES;
+    f4 qpre[PRE_Q ? QN : 1];
+    int pre_seq = -1;
+
+    auto start_seq = [&](const PageEntry& e) {
+        cur = e.seq;
+        first_tis = e.tis;
+        cur_ntiles = e.ntiles;
+        cur_end = e.end;
+        if (PRE_Q && e.seq == pre_seq) {
+            if constexpr (PRE_Q) split_q(qpre);
+            pre_seq = -1;
+        } else {
+            f4 xq[QN];
+            load_q(cur, xq);
+            split_q(xq);
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) o[t] = f4{0.f, 0.f, 0.f, 0.f};
@@ -1227,6 +1252,12 @@ void decode_page_kernel(DecodeParams p) {
                     if (p.table_lens) tlen = min(tlen, p.table_lens[s]);
                     const int end = (int)min((int64_t)ctx, (int64_t)tlen * p.block_size);
                     const int t0 = max(win0, S), t1 = min(win1, S + n);
+                    if constexpr (PRE_Q) {
+                        if (win0 == a && t0 == a) {  // the range's first tile
+                            pre_seq = s;
+                            load_q(s, qpre);
+                        }
+                    }
                     for (int tt = t0 + tid; tt < t1; tt += kPageWaves * 64) {
                         const int tis = tt - S;
                         const int pos = tis * kTile;
