@@ -1084,13 +1084,14 @@ void decode_page_kernel(DecodeParams p) {
             }
         }
     };
-    // fp16 pages: q of the sequence holding the range's first tile is loaded
-    // with the tile list (its wait is the list's), so the first tile does not
-    // wait for the DMA ring the way a later start_seq's load does.  (Byte
-    // pages run 4 waves per SIMD and have no registers for it.)
+    // fp16 pages: q of the first two sequences of the range (the one holding
+    // its first tile, the next one to start in it) is loaded with the tile
+    // list (its wait is the list's), so neither start waits for the DMA ring
+    // the way a later start_seq's load does.  (Byte pages run 4 waves per
+    // SIMD and have no registers for it.)
     constexpr bool PRE_Q = !BYTES;
-    f4 qpre[PRE_Q ? QN : 1];
-    int pre_seq = -1;
+    f4 qpre[PRE_Q ? QN : 1], qpre2[PRE_Q ? QN : 1];
+    int pre_seq = -1, pre_seq2 = -1;
 
     auto start_seq = [&](const PageEntry& e) {
         cur = e.seq;
@@ -1100,6 +1101,9 @@ void decode_page_kernel(DecodeParams p) {
         if (PRE_Q && e.seq == pre_seq) {
             if constexpr (PRE_Q) split_q(qpre);
             pre_seq = -1;
+        } else if (PRE_Q && e.seq == pre_seq2) {
+            if constexpr (PRE_Q) split_q(qpre2);
+            pre_seq2 = -1;
         } else {
             f4 xq[QN];
             load_q(cur, xq);
@@ -1256,6 +1260,9 @@ void decode_page_kernel(DecodeParams p) {
                         if (win0 == a && t0 == a) {  // the range's first tile
                             pre_seq = s;
                             load_q(s, qpre);
+                        } else if (win0 == a && t0 == S && pre_seq2 < 0) {  // next start
+                            pre_seq2 = s;
+                            load_q(s, qpre2);
                         }
                     }
                     for (int tt = t0 + tid; tt < t1; tt += kPageWaves * 64) {
