@@ -51,7 +51,7 @@ def parse():
                     help="skip the config 4 (long context) and config 5 (int8 mixed) legs")
     ap.add_argument("--config-steps", type=int, default=20)
     ap.add_argument("--only", choices=["decode", "prefill", "config4", "config5", "qkprep", "fp8",
-                                       "kvwrite"],
+                                       "kvwrite", "dense"],
                     help="run one leg only and print its JSON (for profiling)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the prefill leg (for profiling its kernel)")
@@ -484,6 +484,38 @@ def bench_kvwrite(torch, pyvcpp, args):
     }
 
 
+def bench_dense(torch, pyvcpp, args):
+    """flash_attention_cuda, the reference's contiguous-KV slot
+    (cuda/attention.cu:58-124, query row 0 of each (batch, head)): 16 x 64
+    (batch, head) pairs over 4096 contiguous fp32 keys, head_dim 80.  Every K
+    and V value is read once and the probabilities written once."""
+    dev = torch.device("cuda:0")
+    B, Hd, kv, ql = 16, H, 4096, 1
+    g = torch.Generator(device=dev).manual_seed(args.seed + 90)
+    q = torch.randn((B, Hd, ql, D), generator=g, device=dev)
+    k = torch.randn((B, Hd, kv, D), generator=g, device=dev)
+    v = torch.randn((B, Hd, kv, D), generator=g, device=dev)
+    out = torch.empty((B, Hd, D), device=dev)
+    w = torch.empty((B * Hd, kv), device=dev)
+    L = pyvcpp.lib()
+
+    def run():
+        L.flash_attention_cuda(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), w.data_ptr(),
+                               B, Hd, D, ql, kv, None)
+    nbytes = B * Hd * (2 * kv * D * 4 + kv * 4 + 2 * D * 4)
+    steps = max(args.config_steps, 20)
+    dt = timed(torch, run, steps)
+    tbs = nbytes / dt / 1e12
+    return {"metric": "flash_attention_cuda HBM TB/s", "value": round(tbs, 3), "unit": "TB/s",
+            "ms_per_step": round(dt * 1e3, 4), "steps": steps,
+            "config": {"workload": "16 x 64 (batch, head) pairs, 4096 contiguous fp32 keys, head_dim 80, "
+                                   "query row 0 per pair (the reference slot's semantics)",
+                       "bytes_per_step": nbytes},
+            "roofline": {"bound": "hbm", "achieved": round(tbs * 1e3, 1), "peak": HBM_PEAK_TBS * 1e3,
+                         "unit": "GB/s", "frac": round(tbs / HBM_PEAK_TBS, 4),
+                         "kernel": "dense_attention_kernel"}}
+
+
 def bench_qkprep(torch, pyvcpp, args):
     """Fused q/k norm + RoPE (vcpp_qk_norm_rope) over config 3's 16384 prefill
     tokens: q [16384][64][80], k [16384][8][80] fp32 at positions 1024..3071,
@@ -563,6 +595,9 @@ def main():
     if args.only == "kvwrite":
         print(json.dumps(bench_kvwrite(torch, pyvcpp, args)))
         return
+    if args.only == "dense":
+        print(json.dumps(bench_dense(torch, pyvcpp, args)))
+        return
 
     w = decode_workload(torch, args.seed)
     pages0 = pyvcpp.kv_pages(pyvcpp.KV_F16, w["sets"][0][0], w["sets"][0][1], BS, HKV, D, w["nb"],
@@ -626,6 +661,7 @@ def main():
         result["qk_prep"] = bench_qkprep(torch, pyvcpp, args)
         result["fp8_decode"] = bench_fp8(torch, pyvcpp, args)
         result["kv_write"] = bench_kvwrite(torch, pyvcpp, args)
+        result["dense"] = bench_dense(torch, pyvcpp, args)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(torch, w, args.cpu_seconds)
         result["cpu_port_threaded"] = cpu_port_threaded(torch, w, min(args.cpu_seconds, 5.0))

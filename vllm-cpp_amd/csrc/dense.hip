@@ -70,11 +70,112 @@ __global__ __launch_bounds__(kThreads) void dense_attention_kernel(DenseParams p
     }
 }
 
+// The same for head_dim % 16 == 0 (<= 128) and 16-byte aligned tensors, laid
+// out for bandwidth.  Logits: lane (key lane / 4, quarter lane % 4) of each
+// wave dots the D / 4 elements of its quarter of a key row (16-byte loads) and
+// the quad sums them with two DPP steps: 16 keys per wave step.  Output: the
+// four waves take a quarter of the keys each, lanes own dims lane and
+// lane + 64, and the quarters are summed through LDS.  Same arithmetic as the
+// generic kernel up to the order of the sums.
+template <int D>
+__global__ __launch_bounds__(kThreads) void dense_attention_vec_kernel(DenseParams p) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    constexpr int EQ = D / 4;       // floats per lane per key row
+    constexpr int NW = kThreads / 64;
+    __shared__ float red[kThreads / 64];
+    __shared__ float part[NW][D];
+    const int64_t bh = blockIdx.x;
+    const int S = p.kv_len;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float* q = p.q + bh * D * p.q_len;
+    const float* k = p.k + bh * D * S;
+    const float* v = p.v + bh * D * S;
+    float* w = p.attn_weights + bh * S;
+    const int qq = lane & 3, r = lane >> 2;
+    f4 qv[EQ / 4];
+#pragma unroll
+    for (int m = 0; m < EQ / 4; ++m) qv[m] = *reinterpret_cast<const f4*>(q + qq * EQ + 4 * m);
+    const float scale = 1.0f / sqrtf((float)D);
+    float mx = -__builtin_inff();
+    for (int s0 = wave * 16; s0 < S; s0 += NW * 16) {
+        const int s = min(s0 + r, S - 1);
+        const float* krow = k + (int64_t)s * D + qq * EQ;
+        float dot = 0.0f;
+#pragma unroll
+        for (int m = 0; m < EQ / 4; ++m) {
+            const f4 x = *reinterpret_cast<const f4*>(krow + 4 * m);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dot += qv[m][i] * x[i];
+        }
+        dot += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, dot), 0xB1, 0xF, 0xF, false));
+        dot += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, dot), 0x4E, 0xF, 0xF, false));
+        float l = dot * scale;
+        if (p.mask && p.mask[s] < 0.0f) l = -1e9f;
+        if (qq == 0 && s0 + r < S) {
+            w[s] = l;
+            mx = fmaxf(mx, l);
+        }
+    }
+    mx = block_reduce(mx, true, red);
+    float sum = 0.0f;
+    for (int s = threadIdx.x; s < S; s += kThreads) {
+        const float e = expf(w[s] - mx);
+        w[s] = e;
+        sum += e;
+    }
+    sum = block_reduce(sum, false, red);
+    const float inv = 1.0f / (sum + 1e-9f);
+    for (int s = threadIdx.x; s < S; s += kThreads) w[s] *= inv;
+    __syncthreads();  // this thread's later reads of w cover other threads' writes
+    const int sa = (int)(((int64_t)S * wave) / NW), sb = (int)(((int64_t)S * (wave + 1)) / NW);
+    // eight keys per step on independent partial sums, so the loads of a
+    // step are all in flight together
+    constexpr int U = 8;
+    float acc0[U] = {}, acc1[U] = {};
+    const bool d1 = lane + 64 < D;
+    int s = sa;
+    for (; s + U <= sb; s += U) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const float ws = w[s + u];
+            const float* vrow = v + (int64_t)(s + u) * D;
+            acc0[u] += ws * vrow[lane];
+            if (d1) acc1[u] += ws * vrow[lane + 64];
+        }
+    }
+    for (; s < sb; ++s) {
+        const float ws = w[s];
+        const float* vrow = v + (int64_t)s * D;
+        acc0[0] += ws * vrow[lane];
+        if (d1) acc1[0] += ws * vrow[lane + 64];
+    }
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        a0 += acc0[u];
+        a1 += acc1[u];
+    }
+    part[wave][lane] = a0;
+    if (d1) part[wave][lane + 64] = a1;
+    __syncthreads();
+    for (int d = threadIdx.x; d < D; d += kThreads) {
+        float o = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) o += part[i][d];
+        p.out[bh * D + d] = o;
+    }
+}
+
 }  // namespace
 
 hipError_t launch_dense(const DenseParams& p, hipStream_t stream) {
-    hipLaunchKernelGGL(dense_attention_kernel, dim3(p.batch * p.heads), dim3(kThreads),
-                       p.head_dim * sizeof(float), stream, p);
+    const dim3 grid(p.batch * p.heads), block(kThreads);
+    auto al = [](const void* x) { return reinterpret_cast<uintptr_t>(x) % 16 == 0; };
+    const bool vec = al(p.q) && al(p.k) && al(p.v) && p.kv_len > 0;
+    if (vec && p.head_dim == 64) hipLaunchKernelGGL(dense_attention_vec_kernel<64>, grid, block, 0, stream, p);
+    else if (vec && p.head_dim == 80) hipLaunchKernelGGL(dense_attention_vec_kernel<80>, grid, block, 0, stream, p);
+    else if (vec && p.head_dim == 128) hipLaunchKernelGGL(dense_attention_vec_kernel<128>, grid, block, 0, stream, p);
+    else hipLaunchKernelGGL(dense_attention_kernel, grid, block, p.head_dim * sizeof(float), stream, p);
     return hipGetLastError();
 }
 
