@@ -66,11 +66,30 @@ def fp8_rows(seed, n):
     return x.reshape(n, HKV, D)
 
 
+def i8_rows(seed, n):
+    """special_rows, plus rows whose int8 quotients x / scale fall exactly on
+    half-integers (round half to even decides) and one float either side of
+    them: the row max is 127 s so the scale is exactly s, for s = 1/8 and for
+    s = fp16(0.1) (their products with k + 1/2 are exact in fp32)."""
+    x = special_rows(seed, n)
+    for r, sc in ((3, 0.125), (4, float(np.float16(0.1)))):
+        for h in range(HKV):
+            ks = np.arange(-40, 40, dtype=np.float64)[: D - 1] + 0.5
+            ties = (ks * sc).astype(np.float32)
+            if h == 1:
+                ties = np.nextafter(ties, np.float32(np.inf))
+            elif h == 2:
+                ties = np.nextafter(ties, np.float32(-np.inf))
+            x[r, h, 0] = np.float32(127 * sc)
+            x[r, h, 1:] = ties[: D - 1]
+    return x
+
+
 @pytest.mark.parametrize("kind,rne", [(O.ORC_F32, 0), (O.ORC_F16, 0), (O.ORC_F16, 1), (O.ORC_I8, 0),
                                       (O.ORC_FP8, 0)])
 def test_write_kv_bit_exact(cuda, kind, rne):
     n = 40
-    rows = fp8_rows if kind == O.ORC_FP8 else special_rows
+    rows = fp8_rows if kind == O.ORC_FP8 else i8_rows if kind == O.ORC_I8 else special_rows
     k = rows(71, n)
     v = rows(72, n)
     slots = O.permutation(73, NB * BS)[:n].astype(np.int64)

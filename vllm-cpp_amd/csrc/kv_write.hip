@@ -187,10 +187,19 @@ __global__ __launch_bounds__(256) void kv_write_vec_kernel(KvWriteParams p, int 
             const uint16_t sh = f16_rne(row_max / 127.0f);
             const float sc = f16_to_f32(sh);
             const float xs[4] = {x.x, x.y, x.z, x.w};
+            // rint(x / sc) with x / sc correctly rounded, as the oracle
+            // computes it.  q = x * fl(1 / sc) is within 2 ulp of fl(x / sc)
+            // (|q| <= 128: 2^-15); when q is more than 2^-14 from every
+            // half-integer no half-integer lies between the two and their
+            // rint agree, otherwise (rarely) divide.
+            const float isc = sc > 0.0f ? 1.0f / sc : 0.0f;
             uint32_t w = 0;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                float r = sc > 0.0f ? rintf(xs[i] / sc) : 0.0f;
+                const float qf = xs[i] * isc;
+                float r = rintf(qf);
+                if (sc > 0.0f && fabsf(fabsf(qf - r) - 0.5f) < 6.103515625e-05f) r = rintf(xs[i] / sc);
+                if (!(sc > 0.0f)) r = 0.0f;
                 r = fminf(fmaxf(r, -127.0f), 127.0f);
                 w |= (uint32_t)(uint8_t)(int8_t)r << (8 * i);
             }
