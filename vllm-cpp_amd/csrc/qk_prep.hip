@@ -223,8 +223,17 @@ __global__ __launch_bounds__(kQkWaves * 64) void qk_prep_lds_kernel(QkPrepParams
         inv = __builtin_amdgcn_rcpf(__builtin_amdgcn_sqrtf(ss * (1.0f / (float)D) + p.eps));
     }
     float y[EQ];
+    if (norm) {
 #pragma unroll
-    for (int i = 0; i < EQ; ++i) y[i] = norm ? T.norm_weight[e0 + i] * x[i] * inv : x[i];
+        for (int m = 0; m < EQ / 4; ++m) {
+            const f4 wv = *reinterpret_cast<const f4*>(T.norm_weight + e0 + 4 * m);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) y[4 * m + i] = wv[i] * x[4 * m + i] * inv;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < EQ; ++i) y[i] = x[i];
+    }
     if (rot) {
         if (half) {
             // partner of e (quarter qq) is e +- P: the same slot of quarter qq ^ 2
@@ -288,7 +297,9 @@ hipError_t launch_qk_prep(const QkPrepParams& p, hipStream_t stream) {
     const int64_t wg = ((int64_t)p.num_tokens * groups + kQkWaves - 1) / kQkWaves;
     const dim3 grid((unsigned)wg), block(kQkWaves * 64);
     const bool aligned = reinterpret_cast<uintptr_t>(p.t[0].x) % 16 == 0 &&
-                         reinterpret_cast<uintptr_t>(p.t[1].x) % 16 == 0;
+                         reinterpret_cast<uintptr_t>(p.t[1].x) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(p.t[0].norm_weight) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(p.t[1].norm_weight) % 16 == 0;
     if (aligned && p.head_dim == 80) hipLaunchKernelGGL(qk_prep_lds_kernel<80>, grid, block, 0, stream, p);
     else if (aligned && p.head_dim == 64) hipLaunchKernelGGL(qk_prep_lds_kernel<64>, grid, block, 0, stream, p);
     else if (aligned && p.head_dim == 128) hipLaunchKernelGGL(qk_prep_lds_kernel<128>, grid, block, 0, stream, p);
