@@ -128,35 +128,34 @@ __global__ __launch_bounds__(kThreads) void dense_attention_vec_kernel(DensePara
     for (int s = threadIdx.x; s < S; s += kThreads) w[s] *= inv;
     __syncthreads();  // this thread's later reads of w cover other threads' writes
     const int sa = (int)(((int64_t)S * wave) / NW), sb = (int)(((int64_t)S * (wave + 1)) / NW);
-    // eight keys per step on independent partial sums, so the loads of a
-    // step are all in flight together
-    constexpr int U = 8;
-    float acc0[U] = {}, acc1[U] = {};
-    const bool d1 = lane + 64 < D;
-    int s = sa;
-    for (; s + U <= sb; s += U) {
+    // lane (row slot lane / EQ, quad lane % EQ) adds w[s] * v[s][4 quad ..] for
+    // the keys s of its slot (R slots per instruction, 16-byte loads)
+    constexpr int R = 64 / EQ;
+    const int slot = lane / EQ, quad = lane - slot * EQ;
+    const bool act = slot < R;
+    f4 acc[2] = {};
+    int s = sa + slot;
+    for (; s + R < sb; s += 2 * R) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const float ws = w[s + u];
-            const float* vrow = v + (int64_t)(s + u) * D;
-            acc0[u] += ws * vrow[lane];
-            if (d1) acc1[u] += ws * vrow[lane + 64];
+        for (int u = 0; u < 2; ++u) {
+            const int su = s + u * R;
+            const float ws = w[su];
+            const f4 x = act ? *reinterpret_cast<const f4*>(v + (int64_t)su * D + 4 * quad) : f4{};
+            acc[u] += ws * x;
         }
     }
-    for (; s < sb; ++s) {
-        const float ws = w[s];
-        const float* vrow = v + (int64_t)s * D;
-        acc0[0] += ws * vrow[lane];
-        if (d1) acc1[0] += ws * vrow[lane + 64];
-    }
-    float a0 = 0.0f, a1 = 0.0f;
+    if (s < sb && act) acc[0] += w[s] * *reinterpret_cast<const f4*>(v + (int64_t)s * D + 4 * quad);
+    const f4 a = acc[0] + acc[1];
+    // sum the R slots of each quad, then the waves, through LDS
+    __shared__ f4 slots_all[NW][64];
+    slots_all[wave][lane] = act ? a : f4{};
+    __syncthreads();
+    if (lane < EQ) {
+        f4 t = {};
+        for (int r = 0; r < R; ++r) t += slots_all[wave][r * EQ + lane];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        a0 += acc0[u];
-        a1 += acc1[u];
+        for (int i = 0; i < 4; ++i) part[wave][4 * lane + i] = t[i];
     }
-    part[wave][lane] = a0;
-    if (d1) part[wave][lane + 64] = a1;
     __syncthreads();
     for (int d = threadIdx.x; d < D; d += kThreads) {
         float o = 0.0f;
