@@ -587,17 +587,26 @@ void prefill_dma_kernel(PrefillParams p) {
     wait_vmcnt<0>();
 
     if (!head_ok) return;
+    // Lane (g, c) holds rows 4 g + r, column 16 t + c.  Column pairs: for the
+    // row pair (2 k, 2 k + 1) even lanes store row 2 k and odd lanes row 2 k + 1,
+    // each the pair (c & ~1, + 1), the other value one DPP swap away.
+    const bool odd = (c & 1) != 0;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
         const float rowsum = sum_over_groups(lsum[rb]);  // row c
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int k2 = 0; k2 < 2; ++k2) {
+            const int r = 2 * k2 + (odd ? 1 : 0);
             const float inv = 1.0f / (shfl(rowsum, 4 * g + r) + 1e-9f);
             const int tok = t0 + 16 * rb + 4 * g + r;
-            if (tok >= n) continue;
-            float* orow = p.out + ((int64_t)(q0 + tok) * p.num_heads + head) * D;
+            float* orow = p.out + ((int64_t)(q0 + min(tok, n - 1)) * p.num_heads + head) * D;
 #pragma unroll
-            for (int t = 0; t < NT; ++t) orow[16 * t + c] = o[rb][t][r] * inv;
+            for (int t = 0; t < NT; ++t) {
+                const float x0 = o[rb][t][2 * k2], x1 = o[rb][t][2 * k2 + 1];
+                const float y = dpp_swap1(odd ? x0 : x1);  // neighbour's value of my row
+                const float2 v = odd ? make_float2(y * inv, x1 * inv) : make_float2(x0 * inv, y * inv);
+                if (tok < n) *reinterpret_cast<float2*>(orow + 16 * t + (c & ~1)) = v;
+            }
         }
     }
 }
