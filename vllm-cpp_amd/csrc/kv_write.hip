@@ -212,6 +212,52 @@ __global__ __launch_bounds__(256) void kv_write_vec_kernel(KvWriteParams p, int 
     }
 }
 
+// fp16 and FP8 pages with head_dim % 8 == 0: eight values per lane (two
+// 16-byte loads of each of K and V), so a lane stores 16 bytes (fp16) or 8
+// (FP8) at once; D / 8 lanes own a row.  Same encoders, element by element.
+template <int KV>
+__global__ __launch_bounds__(256) void kv_write_vec8_kernel(KvWriteParams p, int L, int rows_per_wave) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int seg = lane / L, li = lane - seg * L;
+    if (seg >= rows_per_wave) return;  // whole segments idle
+    const int64_t item = ((int64_t)blockIdx.x * 4 + wave) * rows_per_wave + seg;
+    if (item >= (int64_t)p.num_tokens * p.num_kv_heads) return;
+    const int64_t tok = item / p.num_kv_heads;
+    const int h = (int)(item - tok * p.num_kv_heads);
+    const int64_t slot = p.slots[tok];
+    if (slot < 0) return;
+    const int64_t block = slot / p.block_size;
+    if (block >= p.num_blocks) return;
+    const int pos = (int)(slot - block * p.block_size);
+    const int D = p.head_dim;
+    const int64_t src_off = (tok * p.num_kv_heads + h) * D + 8 * li;
+    const int64_t dst_off = block * p.block_stride + ((int64_t)pos * p.num_kv_heads + h) * D + 8 * li;
+    for (int which = 0; which < 2; ++which) {
+        const float* src = (which ? p.v_src : p.k_src) + src_off;
+        const float4 a = *reinterpret_cast<const float4*>(src);
+        const float4 b = *reinterpret_cast<const float4*>(src + 4);
+        const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        void* base = which ? p.v : p.k;
+        if constexpr (KV == VCPP_KV_F16) {
+            uint32_t w[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint16_t e0 = p.fp16_rne ? f16_rne(xs[2 * i]) : f16_trunc(xs[2 * i]);
+                const uint16_t e1 = p.fp16_rne ? f16_rne(xs[2 * i + 1]) : f16_trunc(xs[2 * i + 1]);
+                w[i] = e0 | ((uint32_t)e1 << 16);
+            }
+            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + dst_off) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+            uint32_t w[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                w[i] = fp8_encode(xs[4 * i]) | ((uint32_t)fp8_encode(xs[4 * i + 1]) << 8) |
+                       ((uint32_t)fp8_encode(xs[4 * i + 2]) << 16) | ((uint32_t)fp8_encode(xs[4 * i + 3]) << 24);
+            *reinterpret_cast<uint2*>(static_cast<uint8_t*>(base) + dst_off) = make_uint2(w[0], w[1]);
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_kv_write(const KvWriteParams& p, hipStream_t stream) {
@@ -222,6 +268,18 @@ hipError_t launch_kv_write(const KvWriteParams& p, hipStream_t stream) {
     const bool vec = p.head_dim % 4 == 0 && p.head_dim <= 256 && p.block_stride % 4 == 0 &&
                      aligned(p.k_src, 16) && aligned(p.v_src, 16) && aligned(p.k, 4 * es) &&
                      aligned(p.v, 4 * es);
+    const bool vec8 = vec && (p.dtype == VCPP_KV_F16 || p.dtype == VCPP_KV_FP8) && p.head_dim % 8 == 0 &&
+                      p.block_stride % 8 == 0 && aligned(p.k, 8 * es) && aligned(p.v, 8 * es);
+    if (vec8) {
+        const int L = p.head_dim / 8, rpw = 64 / L;
+        const int64_t waves = (items + rpw - 1) / rpw;
+        const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+        if (p.dtype == VCPP_KV_F16)
+            hipLaunchKernelGGL(kv_write_vec8_kernel<VCPP_KV_F16>, grid, block, 0, stream, p, L, rpw);
+        else
+            hipLaunchKernelGGL(kv_write_vec8_kernel<VCPP_KV_FP8>, grid, block, 0, stream, p, L, rpw);
+        return hipGetLastError();
+    }
     if (vec) {
         const int L = p.head_dim / 4, rpw = 64 / L;
         const int64_t waves = (items + rpw - 1) / rpw;
