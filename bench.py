@@ -479,7 +479,7 @@ def bench_kvwrite(torch, pyvcpp, args):
         "config": {"workload": "config 3 chunk tokens: 16384 x 8 kv heads x 80, K and V fp32 -> pages "
                                "(value: fp16, the reference's truncating encoder)"},
         "roofline": {"bound": "hbm", "achieved": round(f["TB/s"] * 1e3, 1), "peak": HBM_PEAK_TBS * 1e3,
-                     "unit": "GB/s", "frac": round(f["TB/s"] / HBM_PEAK_TBS, 4), "kernel": "kv_write_vec_kernel"},
+                     "unit": "GB/s", "frac": round(f["TB/s"] / HBM_PEAK_TBS, 4), "kernel": "kv_write_vec8_kernel"},
         "variants": out,
     }
 
