@@ -552,7 +552,7 @@ def bench_qkprep(torch, pyvcpp, args):
                    "bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(nbytes / k_s / 1e9, 1), "peak": HBM_PEAK_TBS * 1e3,
                      "unit": "GB/s", "frac": round(nbytes / k_s / 1e12 / HBM_PEAK_TBS, 4),
-                     "kernel": "qk_prep_kernel", "kernel_avg_us": round(k_s * 1e6, 2)},
+                     "kernel": "qk_prep_lds_kernel<80>", "kernel_avg_us": round(k_s * 1e6, 2)},
     }
 
 

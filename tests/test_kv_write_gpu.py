@@ -172,12 +172,17 @@ def test_write_then_prefill(cuda, kind):
     assert_close(got, want, 2e-3, 1e-2, what="write then prefill kind=%d" % kind)
 
 
+@pytest.mark.parametrize("d", [10, 16, 24, 40, 64, 128])
 @pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8, O.ORC_FP8])
-def test_write_kv_generic_path(cuda, kind):
-    """head_dim 10 (not a multiple of 4): the one-wave-per-row writer."""
-    nb, bs, hkv, d, n = 6, 16, 3, 10, 50
-    x = O.normal(91, (n, hkv, d), 0.0, 4.0)
-    y = O.normal(92, (n, hkv, d), 0.0, 4.0)
+def test_write_kv_head_dims(cuda, kind, d):
+    """Head dims that pick each writer: 10 (not a multiple of 4) the
+    one-wave-per-row kernel; 24 and 40 eight values per lane on an odd lane
+    count per row for fp16 / FP8, four per lane for int8; 16, 64, 128 eight
+    per lane on an even lane count."""
+    nb, bs, hkv, n = 6, 16, 3, 50
+    x = O.normal(91 + d, (n, hkv, d), 0.0, 4.0)
+    y = O.normal(92 + d, (n, hkv, d), 0.0, 4.0)
+    x[3, 1] *= 1e-6  # a tiny row next to ordinary ones
     slots = O.permutation(93, nb * bs)[:n].astype(np.int64)
     shape = (nb, bs, hkv, d)
     if kind == O.ORC_F16:

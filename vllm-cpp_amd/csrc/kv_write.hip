@@ -212,9 +212,11 @@ __global__ __launch_bounds__(256) void kv_write_vec_kernel(KvWriteParams p, int 
     }
 }
 
-// fp16 and FP8 pages with head_dim % 8 == 0: eight values per lane (two
+// fp16, int8 and FP8 pages with head_dim % 8 == 0: eight values per lane (two
 // 16-byte loads of each of K and V), so a lane stores 16 bytes (fp16) or 8
-// (FP8) at once; D / 8 lanes own a row.  Same encoders, element by element.
+// (int8, FP8) at once; D / 8 lanes own a row.  Same encoders, element by
+// element; the int8 row max is exact in any order (a lane-pair DPP swap, then
+// one read per pair: rows start on even lanes).
 template <int KV>
 __global__ __launch_bounds__(256) void kv_write_vec8_kernel(KvWriteParams p, int L, int rows_per_wave) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -247,6 +249,33 @@ __global__ __launch_bounds__(256) void kv_write_vec8_kernel(KvWriteParams p, int
                 w[i] = e0 | ((uint32_t)e1 << 16);
             }
             *reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + dst_off) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else if constexpr (KV == VCPP_KV_I8) {
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(xs[i]));
+            const float pm = fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                             0, __builtin_bit_cast(int, amax), 0xB1, 0xF, 0xF, false)));
+            float row_max = pm;
+            for (int j = 0; j < L; j += 2) row_max = fmaxf(row_max, __shfl(pm, seg * L + j, 64));
+            const uint16_t sh = f16_rne(row_max / 127.0f);
+            const float sc = f16_to_f32(sh);
+            // rint(x / sc), x / sc correctly rounded: see kv_write_vec_kernel
+            const float isc = sc > 0.0f ? 1.0f / sc : 0.0f;
+            uint32_t w[2] = {0u, 0u};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float qf = xs[i] * isc;
+                float r = rintf(qf);
+                if (sc > 0.0f && fabsf(fabsf(qf - r) - 0.5f) < 6.103515625e-05f) r = rintf(xs[i] / sc);
+                if (!(sc > 0.0f)) r = 0.0f;
+                r = fminf(fmaxf(r, -127.0f), 127.0f);
+                w[i >> 2] |= (uint32_t)(uint8_t)(int8_t)r << (8 * (i & 3));
+            }
+            *reinterpret_cast<uint2*>(static_cast<int8_t*>(base) + dst_off) = make_uint2(w[0], w[1]);
+            if (li == 0) {
+                uint16_t* scp = which ? p.v_scale : p.k_scale;
+                scp[block * p.scale_block_stride + (int64_t)h * p.block_size + pos] = sh;
+            }
         } else {
             uint32_t w[2];
 #pragma unroll
@@ -268,7 +297,9 @@ hipError_t launch_kv_write(const KvWriteParams& p, hipStream_t stream) {
     const bool vec = p.head_dim % 4 == 0 && p.head_dim <= 256 && p.block_stride % 4 == 0 &&
                      aligned(p.k_src, 16) && aligned(p.v_src, 16) && aligned(p.k, 4 * es) &&
                      aligned(p.v, 4 * es);
-    const bool vec8 = vec && (p.dtype == VCPP_KV_F16 || p.dtype == VCPP_KV_FP8) && p.head_dim % 8 == 0 &&
+    // int8's pair-swap row max needs rows to start on even lanes: D / 8 even
+    const bool vec8 = vec && p.dtype != VCPP_KV_F32 && p.head_dim % (p.dtype == VCPP_KV_I8 ? 16 : 8) == 0 &&
+                      p.head_dim >= 16 &&
                       p.block_stride % 8 == 0 && aligned(p.k, 8 * es) && aligned(p.v, 8 * es);
     if (vec8) {
         const int L = p.head_dim / 8, rpw = 64 / L;
@@ -276,6 +307,8 @@ hipError_t launch_kv_write(const KvWriteParams& p, hipStream_t stream) {
         const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
         if (p.dtype == VCPP_KV_F16)
             hipLaunchKernelGGL(kv_write_vec8_kernel<VCPP_KV_F16>, grid, block, 0, stream, p, L, rpw);
+        else if (p.dtype == VCPP_KV_I8)
+            hipLaunchKernelGGL(kv_write_vec8_kernel<VCPP_KV_I8>, grid, block, 0, stream, p, L, rpw);
         else
             hipLaunchKernelGGL(kv_write_vec8_kernel<VCPP_KV_FP8>, grid, block, 0, stream, p, L, rpw);
         return hipGetLastError();
