@@ -65,24 +65,16 @@ __device__ uint8_t fp8_encode(float v) {
         }
         return (uint8_t)(sign | best);
     }
-    // The largest code c with value <= a, and c + 1; both errors are exact
-    // (the values lie within a factor 2 of a), so the nearest wins and a tie
-    // keeps c, as the reference's first-minimum search does.
-    uint32_t c;
-    float lo, step;
-    if (a < 0.015625f) {  // subnormal codes, multiples of 2^-9
-        c = (uint32_t)(a * 512.0f);
-        lo = (float)c * (1.0f / 512.0f);
-        step = 1.0f / 512.0f;
-    } else {
-        const uint32_t b = fbits(a);
-        const int e = (int)(b >> 23) - 127;  // -6 .. 7
-        c = ((uint32_t)(e + 7) << 3) | ((b >> 20) & 7u);
-        lo = __builtin_bit_cast(float, b & 0xFFF00000u);
-        step = __builtin_bit_cast(float, (uint32_t)(e - 3 + 127) << 23);
-    }
-    const float hi = lo + step;
-    return (uint8_t)(sign | ((hi - a) < (a - lo) ? c + 1 : c));
+    // Nearest code, a tie keeping the smaller one (the reference's search
+    // takes the first minimum over ascending codes).  Normal codes: the
+    // float's top 12 bits are (exponent, 3 mantissa bits), so adding half a
+    // code step minus one unit and shifting rounds half down, a carry moving
+    // into the exponent; E4M3's bias 7 is 120 below fp32's.  Subnormal codes
+    // are multiples of 2^-9: ceil(x - 1/2) rounds x = 512 a half down (x - 1/2
+    // is exact for x >= 1/4, and below that either way rounds to 0).
+    const uint32_t c = a < 0.015625f ? (uint32_t)__builtin_ceilf(a * 512.0f - 0.5f)
+                                     : ((fbits(a) + 0x7FFFFu) >> 20) - (120u << 3);
+    return (uint8_t)(sign | c);
 }
 
 __global__ __launch_bounds__(256) void kv_write_kernel(KvWriteParams p) {
