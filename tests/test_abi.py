@@ -132,3 +132,12 @@ def test_qk_prep_argument_errors():
     assert "NULL" in pyvcpp.last_error()
     L.apply_rope_cuda(p, p, p, p, 160, 1, 2)
     assert "head_dim 1" in pyvcpp.last_error()
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    """No fallback path: without the built library the loader raises (and so
+    does every op that needs it) instead of computing anything elsewhere."""
+    monkeypatch.setattr(pyvcpp, "_lib", None)
+    monkeypatch.setattr(pyvcpp, "LIB_PATH", str(tmp_path / "absent" / "libvcpp_attn.so"))
+    with pytest.raises(RuntimeError, match="not built"):
+        pyvcpp.lib()
