@@ -26,13 +26,16 @@ namespace {
 __device__ __forceinline__ uint32_t fbits(float x) { return __builtin_bit_cast(uint32_t, x); }
 
 __device__ uint16_t f16_trunc(float x) {
-    const uint32_t b = fbits(x);
-    const uint32_t s = b >> 31, e = (b >> 23) & 0xFFu, f = b & 0x7FFFFFu;
-    if (e == 0xFFu) return (uint16_t)((s << 15) | (0x1Fu << 10) | (f ? 1u : 0u));
-    const int ee = (int)e - 127 + 15;
-    if (e == 0 || ee <= 0) return (uint16_t)(s << 15);
-    if (ee >= 31) return (uint16_t)((s << 15) | (0x1Fu << 10));
-    return (uint16_t)((s << 15) | ((uint32_t)ee << 10) | ((f >> 13) & 0x3FFu));
+    // The reference's truncating encoder on |x|'s bits: NaN keeps a quiet
+    // payload of 1, exponents past fp16's (and inf) give inf, those below its
+    // normal range give zero (no subnormals), the rest drop 13 mantissa bits
+    // and rebias the exponent (fp32's bias 127 is 112 above fp16's).
+    const uint32_t b = fbits(x), a = b & 0x7FFFFFFFu;
+    const uint32_t mag = a > 0x7F800000u   ? 0x7C01u
+                         : a >= 0x47800000u ? 0x7C00u
+                         : a < 0x38800000u  ? 0u
+                                            : (a >> 13) - (112u << 10);
+    return (uint16_t)(((b >> 16) & 0x8000u) | mag);
 }
 
 __device__ uint16_t f16_rne(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
