@@ -26,8 +26,9 @@
 //  * Every K/V page is read from HBM once for a kv head's whole GQA group.
 //  * Balanced split: the 16-token tiles of all sequences are laid end to end
 //    and every resident workgroup takes an equal contiguous range of them, so
-//    ragged batches keep the whole GPU busy to the end.  A range touches 1-3
-//    sequences; a sequence wholly inside one range is finished in place, and
+//    ragged batches keep the whole GPU busy to the end.  A range touches one
+//    or more sequences (1-3 for 64 sequences of U[128, 4096] tokens over 256
+//    ranges); a sequence wholly inside one range is finished in place, and
 //    at most two fragments per range (the sequence continuing from the
 //    previous range, the one continuing into the next) leave (m, l, o)
 //    partials that a log-sum-exp merge kernel combines.
@@ -803,8 +804,8 @@ __global__ __launch_bounds__(256) void merge_parts_kernel(DecodeParams p) {
 // merge_split_kernel.
 //
 // int8 and FP8 pages (one byte per value): K fragments are widened to fp16 in
-// registers (int8: exact integers; FP8: its values) and each wave widens its
-// head's V rows into a private fp16 tile for the transposing reads.  int8
+// registers (int8: exact integers; FP8: its values), and V is read transposed
+// straight from the byte tile (ds_read_b64_tr_b8) and widened likewise.  int8
 // pages also carry the tile's 8 x 16 K and V scales (fp16, [head][token]) in
 // one more DMA instruction: the K scale multiplies the fp32 score, the V scale
 // fp32 P before its fp16 split.
