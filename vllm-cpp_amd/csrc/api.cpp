@@ -49,7 +49,8 @@ constexpr int64_t kMinTilesPerRange = 4;
 constexpr int64_t kMaxRanges = 1 << 20;
 // Page-staged decode: the balanced split charges each sequence this many
 // 16-token tiles for starting it (its Q load, the previous one's outputs).  A
-// sweep of 0, 2, 4, 6, 8 on BASELINE config 2 put the step's best at 2.
+// sweep of 0, 2, 4, 6, 8 on BASELINE config 2 put the step's best at 2; byte
+// pages (half the bytes per tile) measured the same at 2, 3 and 4.
 constexpr int kSwitchTiles = 2;
 
 int32_t ceil_div(int64_t a, int64_t b) { return (int32_t)((a + b - 1) / b); }
