@@ -65,6 +65,11 @@ const char* vcpp_version(void);
  * block_stride = num_layers * block_size * kv_dim.
  * VCPP_KV_I8 adds fp16 scale pages: block b's K scales are
  *   k_scale + b * scale_block_stride,  laid out [num_kv_heads][block_size].
+ * VCPP_KV_F16 pages are read as IEEE binary16: a NaN code (which the
+ * reference encoder writes for a NaN input as 0x7C01 and its decoder,
+ * src/kv_cache_manager.cpp:136-137, reads back as +-inf) is a NaN here, so a
+ * non-finite K or V input gives NaN outputs where the reference gives inf or
+ * NaN.  Finite codes decode identically.
  * VCPP_KV_FP8 pages hold one byte per value and no scales.  Codes with
  * exponent 15 (the reference's +-inf and NaN, which its encoder produces only
  * from non-finite inputs) are read by the attention kernels as the OCP E4M3
@@ -215,13 +220,15 @@ int vcpp_head_norm(float* x, const float* weight, float eps, int32_t num_rows, i
  * cuda/attention.h:19-30.  Defined here (the reference leaves these open):
  *   q, out        [batch_size][num_heads][head_dim] fp32
  *   kv_cache      fp16 pages [num_blocks][2 (K, V)][block_size][num_kv_heads][head_dim]
- *                 (K and V behind the one pointer; num_blocks is not passed,
- *                 so block ids are trusted)
+ *                 (K and V behind the one pointer; num_blocks is not passed:
+ *                 ids whose block would end past the device allocation that
+ *                 holds kv_cache are skipped, hipMemGetAddressRange)
  *   block_tables  [batch_size][max_b ceil(context_lens[b] / block_size)] int32
  *   context_lens  HOST int32 [batch_size] (the reference reads it on the host,
  *                 cuda/attention.cu:25-28); the library stages a device copy.
  *   block_size    16 or 32; anything else launches nothing and records
- *                 VCPP_E_UNSUPPORTED in vcpp_last_error().
+ *                 VCPP_E_UNSUPPORTED in vcpp_last_error(), as do head counts
+ *                 that are not positive multiples (VCPP_E_INVALID).
  * Runs on the null stream, asynchronously; uses a library-owned workspace.
  */
 void paged_attention_cuda(const float* q, const uint16_t* kv_cache, const int32_t* block_tables,

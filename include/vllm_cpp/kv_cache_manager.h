@@ -24,6 +24,8 @@
 #include "kv_config.h"
 #include "vcpp_attention.h"
 
+struct PoolStaging;  // device staging of the paged_attention.h entry points
+
 inline constexpr int32_t kv_elem_size(KVDtype dtype) {
     switch (dtype) {
         case KVDtype::FP32: return 4;
@@ -101,8 +103,11 @@ public:
     // ---- device extensions (no reference counterpart) ----
     // Page descriptor of one layer for the vcpp_* kernels.
     vcpp_kv_pages pages(int32_t layer) const;
-    void set_stream(void* stream) { stream_ = stream; }
+    // Work queued by later calls goes to `stream`; set_stream first waits
+    // for the previous stream, which the pool's staging buffers may be in use on.
+    void set_stream(void* stream);
     void* stream() const { return stream_; }
+    PoolStaging& staging() const { return *staging_; }
 
 private:
     void zero_block(int32_t block_id);
@@ -121,6 +126,7 @@ private:
     uint16_t* v_scale_ = nullptr;
     void* stream_ = nullptr;
 
+    std::unique_ptr<PoolStaging> staging_;
     mutable std::vector<float> k_convert_buf_;
     mutable std::vector<float> v_convert_buf_;
     mutable std::mutex mtx_;

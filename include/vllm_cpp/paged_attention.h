@@ -34,7 +34,33 @@ void write_kv_token(KVCacheManager& kv_manager, const std::vector<int32_t>& bloc
 void write_kv_prefill(KVCacheManager& kv_manager, const std::vector<int32_t>& block_table,
                       int32_t seq_len, int32_t layer, const float* k_data, const float* v_data);
 
-// Host outputs [seq_len][kv_dim] floats (positions past the table are left as is).
+// Host outputs [seq_len][kv_dim] floats (positions past the table are left as
+// is): one device gather of the rows and one copy to the host.
 void read_kv_prefill(const BlockPool& kv_manager, const std::vector<int32_t>& block_table,
                      int32_t seq_len, int32_t layer, int32_t num_kv_heads, int32_t head_dim,
                      float* k_out, float* v_out);
+
+// Causal attention of num_tokens new tokens of one sequence appended to
+// prefix_len tokens already in its blocks: row i of q ([num_tokens][num_heads
+// * head_dim] fp32, host or device) attends positions 0 .. prefix_len + i
+// through block_table, into row i of out.  The chunk's K/V must be in the
+// pool already (write_kv_prefill).  This is the engine's prefill loop of
+// read_kv_prefill + compute_attention per position
+// (src/paged_engine.cpp:381-384, src/paged_attention.cpp:174-201) as one
+// launch: q is rounded to fp16 for the MFMA kernel (vcpp_paged_prefill) on
+// FP16 / FP8 / INT8 pools; FP32 pools run every row as an fp32 decode query.
+void paged_prefill(const float* q, const std::vector<int32_t>& block_table, int32_t prefix_len,
+                   int32_t num_tokens, const BlockPool& kv_manager, int32_t num_heads,
+                   int32_t num_kv_heads, int32_t head_dim, int32_t layer, float* out);
+
+// Several sequences' chunks in one launch (a ScheduleOutput's prefills,
+// src/scheduler.h:14-23).  Chunks without a table or tokens are skipped.
+struct PrefillChunk {
+    const float* q;                          // [num_tokens][num_heads * head_dim]
+    const std::vector<int32_t>* block_table;
+    int32_t prefix_len;
+    int32_t num_tokens;
+    float* out;                              // [num_tokens][num_heads * head_dim]
+};
+void paged_prefill_batch(const std::vector<PrefillChunk>& chunks, const BlockPool& kv_manager,
+                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t layer);

@@ -39,16 +39,26 @@ std::vector<float> normal(uint64_t seed, size_t n, double std = 1.0) {
     return x;
 }
 
+// The parity bar: max |got - want| <= atol outright, and the normwise
+// relative error ||got - want|| / ||want|| <= rtol.
 void close(const float* got, const float* want, size_t n, double atol, double rtol, const char* what) {
-    double worst = 0;
+    double worst = 0, e2 = 0, w2 = 0;
+    size_t at = 0;
     for (size_t i = 0; i < n; ++i) {
-        const double err = std::fabs((double)got[i] - want[i]);
         CHECK(std::isfinite(got[i]), "%s: non-finite at %zu", what, i);
-        CHECK(err <= atol + rtol * std::fabs((double)want[i]), "%s: index %zu got %.7g want %.7g", what,
-              i, got[i], want[i]);
-        worst = std::max(worst, err);
+        const double err = std::fabs((double)got[i] - want[i]);
+        if (err > worst) {
+            worst = err;
+            at = i;
+        }
+        e2 += err * err;
+        w2 += (double)want[i] * want[i];
     }
-    std::printf("ok   %-58s max abs err %.3g\n", what, worst);
+    CHECK(worst <= atol, "%s: max abs err %.3g > %.3g at index %zu (got %.7g want %.7g)", what, worst, atol, at,
+          got[at], want[at]);
+    const double rel = w2 > 0 ? std::sqrt(e2 / w2) : std::sqrt(e2);
+    CHECK(rel <= rtol, "%s: normwise relative err %.3g > %.3g", what, rel, rtol);
+    std::printf("ok   %-58s max abs err %.3g, rel %.3g\n", what, worst, rel);
 }
 
 // Host image of one layer of a pool in the reference slab layout, encoded by
@@ -306,8 +316,107 @@ void test_attention(KVDtype dt) {
         }
     }
     std::printf("ok   %-58s\n", "read_kv_prefill");
+    // 6. paged_prefill: the last 200 tokens of request 3 as one chunk on its
+    // 577-token prefix, host fp32 q and out (the engine's prefill buffers);
+    // row i is the reference's per-position attention over 0 .. 577 + i.
+    {
+        const int32_t n = 200, pre = lens[3] - n;
+        std::vector<float> qc = normal(400, (size_t)n * H * D), wc((size_t)n * H * D), gc((size_t)n * H * D, NAN);
+        for (int32_t i = 0; i < n; ++i)
+            orc_paged_attention(&op, qc.data() + (size_t)i * H * D, tables[3].data(), (int32_t)tables[3].size(),
+                                pre + i + 1, H, wc.data() + (size_t)i * H * D);
+        paged_prefill(qc.data(), tables[3], pre, n, m.block_pool(), H, HKV, D, layer, gc.data());
+        close(gc.data(), wc.data(), gc.size(), tol, rtol, "paged_prefill, host buffers");
+        // 7. two chunks in one launch, device q / out: request 1 whole
+        // (prefix 0) and request 3's chunk again.
+        const int32_t n1 = lens[1];
+        std::vector<float> q1 = normal(401, (size_t)n1 * H * D), w1((size_t)n1 * H * D);
+        for (int32_t i = 0; i < n1; ++i)
+            orc_paged_attention(&op, q1.data() + (size_t)i * H * D, tables[1].data(), (int32_t)tables[1].size(),
+                                i + 1, H, w1.data() + (size_t)i * H * D);
+        float *q1d, *o1d, *qcd, *ocd;
+        CHECK(hipMalloc(&q1d, q1.size() * 4) == hipSuccess && hipMalloc(&o1d, q1.size() * 4) == hipSuccess &&
+                  hipMalloc(&qcd, qc.size() * 4) == hipSuccess && hipMalloc(&ocd, qc.size() * 4) == hipSuccess,
+              "malloc");
+        CHECK(hipMemcpy(q1d, q1.data(), q1.size() * 4, hipMemcpyHostToDevice) == hipSuccess &&
+                  hipMemcpy(qcd, qc.data(), qc.size() * 4, hipMemcpyHostToDevice) == hipSuccess,
+              "copy");
+        paged_prefill_batch({{q1d, &tables[1], 0, n1, o1d}, {qcd, &tables[3], pre, n, ocd}}, m.block_pool(), H,
+                            HKV, D, layer);
+        CHECK(hipDeviceSynchronize() == hipSuccess, "sync");
+        std::vector<float> g1(q1.size());
+        CHECK(hipMemcpy(g1.data(), o1d, g1.size() * 4, hipMemcpyDeviceToHost) == hipSuccess &&
+                  hipMemcpy(gc.data(), ocd, gc.size() * 4, hipMemcpyDeviceToHost) == hipSuccess,
+              "copy");
+        close(g1.data(), w1.data(), g1.size(), tol, rtol, "paged_prefill_batch chunk 0, device buffers");
+        close(gc.data(), wc.data(), gc.size(), tol, rtol, "paged_prefill_batch chunk 1, device buffers");
+        for (float* p : {q1d, o1d, qcd, ocd}) (void)hipFree(p);
+    }
     (void)hipFree(qd);
     (void)hipFree(od);
+}
+
+// Two pools on two streams, device q / out, calls queued back to back with no
+// wait between them: each pool stages its own arguments, so neither call can
+// see the other's tables, lengths or partials.
+void test_two_pools_two_streams() {
+    const int32_t L = 1, H = 64, HKV = 8, D = 80, kv = HKV * D, NB = 120;
+    const int32_t lens[2][3] = {{1000, 33, 400}, {17, 1500, 260}};
+    hipStream_t st[2];
+    CHECK(hipStreamCreate(&st[0]) == hipSuccess && hipStreamCreate(&st[1]) == hipSuccess, "streams");
+    KVCacheManager m0(L, kv, NB, KVDtype::FP16, D), m1(L, kv, NB, KVDtype::FP16, D);
+    KVCacheManager* ms[2] = {&m0, &m1};
+    std::vector<HostLayer> hosts{HostLayer(KVDtype::FP16, NB, L, HKV, D), HostLayer(KVDtype::FP16, NB, L, HKV, D)};
+    std::vector<std::vector<int32_t>> tables[2];
+    std::vector<float> want[2], q[2];
+    float *qd[2], *od[2];
+    for (int i = 0; i < 2; ++i) {
+        tables[i].resize(3);
+        for (int r = 0; r < 3; ++r) {
+            CHECK(ms[i]->alloc_blocks((lens[i][r] + 15) / 16, tables[i][r]), "alloc");
+            auto k = normal(500 + 10 * i + r, (size_t)lens[i][r] * kv), v = normal(600 + 10 * i + r, (size_t)lens[i][r] * kv);
+            write_kv_prefill(*ms[i], tables[i][r], lens[i][r], 0, k.data(), v.data());
+            for (int32_t p = 0; p < lens[i][r]; ++p)
+                hosts[i].write(tables[i][r][p / 16], 0, p % 16, k.data() + (size_t)p * kv, v.data() + (size_t)p * kv);
+        }
+        ms[i]->block_pool().set_stream(st[i]);
+        q[i] = normal(700 + i, (size_t)3 * H * D);
+        want[i].resize(q[i].size());
+        orc_pool op = hosts[i].pool(0);
+        for (int r = 0; r < 3; ++r)
+            orc_paged_attention(&op, q[i].data() + (size_t)r * H * D, tables[i][r].data(),
+                                (int32_t)tables[i][r].size(), lens[i][r], H, want[i].data() + (size_t)r * H * D);
+        CHECK(hipMalloc(&qd[i], q[i].size() * 4) == hipSuccess && hipMalloc(&od[i], q[i].size() * 4) == hipSuccess,
+              "malloc");
+        CHECK(hipMemcpy(qd[i], q[i].data(), q[i].size() * 4, hipMemcpyHostToDevice) == hipSuccess, "copy");
+    }
+    CHECK(hipDeviceSynchronize() == hipSuccess, "sync");
+    for (int rep = 0; rep < 4; ++rep)
+        for (int i = 0; i < 2; ++i) {
+            std::vector<const float*> qp;
+            std::vector<float*> opp;
+            std::vector<const std::vector<int32_t>*> tp;
+            std::vector<int32_t> sl;
+            for (int r = 0; r < 3; ++r) {
+                qp.push_back(qd[i] + (size_t)r * H * D);
+                opp.push_back(od[i] + (size_t)r * H * D);
+                tp.push_back(&tables[i][r]);
+                sl.push_back(lens[i][r]);
+            }
+            paged_attention_batch(qp, tp, sl, ms[i]->block_pool(), H, HKV, D, 0, opp);
+        }
+    CHECK(hipDeviceSynchronize() == hipSuccess, "sync");
+    for (int i = 0; i < 2; ++i) {
+        std::vector<float> got(q[i].size());
+        CHECK(hipMemcpy(got.data(), od[i], got.size() * 4, hipMemcpyDeviceToHost) == hipSuccess, "copy");
+        close(got.data(), want[i].data(), got.size(), 2e-3, 1e-2,
+              i ? "two pools on two streams: pool 1" : "two pools on two streams: pool 0");
+        (void)hipFree(qd[i]);
+        (void)hipFree(od[i]);
+        ms[i]->block_pool().set_stream(nullptr);
+    }
+    (void)hipStreamDestroy(st[0]);
+    (void)hipStreamDestroy(st[1]);
 }
 
 }  // namespace
@@ -327,6 +436,7 @@ int main() {
         std::printf("---- attention on %s pages\n", names[(int)dt]);
         test_attention(dt);
     }
+    test_two_pools_two_streams();
     std::printf("ALL PASSED (%d checks)\n", g_checks);
     return 0;
 }

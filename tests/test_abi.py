@@ -90,6 +90,24 @@ def test_v1_rejects_block_size():
     assert "block_size" in pyvcpp.last_error()
 
 
+@pytest.mark.parametrize("heads,frag", [((64, 0), "num_kv_heads"), ((0, 8), "num_kv_heads"),
+                                        ((60, 8), "num_kv_heads"), ((64, -8), "num_kv_heads")])
+def test_v1_rejects_head_counts(heads, frag):
+    """Head counts are checked before anything divides by them."""
+    L = pyvcpp.lib()
+    ctx = (ctypes.c_int32 * 1)(16)
+    L.paged_attention_cuda(4096, 4096, 4096, ctypes.addressof(ctx), 4096, heads[0], heads[1], 80,
+                           16, 1)
+    assert frag in pyvcpp.last_error()
+
+
+def test_v1_rejects_head_dim():
+    L = pyvcpp.lib()
+    ctx = (ctypes.c_int32 * 1)(16)
+    L.paged_attention_cuda(4096, 4096, 4096, ctypes.addressof(ctx), 4096, 64, 8, 72, 16, 1)
+    assert "head_dim 72" in pyvcpp.last_error()
+
+
 def test_flash_rejects_empty_kv():
     """kv_len 0 would read an unset logit in the reference; here it records
     VCPP_E_INVALID before any HIP call."""

@@ -1,7 +1,7 @@
 """GPU parity of the paged decode path (vcpp_paged_decode / paged_attention_cuda)
 against the CPU oracle on identical seeded inputs.
 
-Tolerances (numpy allclose form, err <= atol + rtol * |want|):
+Tolerances (max-abs error <= atol, and normwise relative error <= rtol):
   fp32 KV: atol 1e-4, rtol 1e-4;  fp16 / int8 / fp8 KV: atol 2e-3, rtol 1e-2.
 """
 import numpy as np
@@ -159,11 +159,52 @@ def test_v1_entry(cuda):
     assert_close(out.cpu().numpy(), want, *TOL[O.ORC_F16], what="v1")
 
 
+def _allocation_end(ptr):
+    """End address of the device allocation holding ptr (hipMemGetAddressRange)."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    base, size = ctypes.c_void_p(), ctypes.c_size_t()
+    rc = hip.hipMemGetAddressRange(ctypes.byref(base), ctypes.byref(size), ctypes.c_void_p(ptr))
+    assert rc == 0 and base.value, "hipMemGetAddressRange failed (%d)" % rc
+    return base.value + size.value
+
+
+def test_v1_skips_ids_past_the_allocation(cuda):
+    """v1 carries no block count: block ids whose page would end past the
+    allocation that holds kv_cache are skipped, as the reference's get_k skips
+    ids outside the pool (src/kv_cache_manager.cpp:90-95)."""
+    nb = 40
+    pool = O.make_pool(O.ORC_F16, 91, nb, 8, 80)
+    ctx = np.array([200, 64], dtype=np.int32)
+    q = O.normal(93, (2, 64, 80))
+    tables = random_tables(95, ctx, nb)
+    kv = np.stack([pool.k, pool.v], axis=1)
+    kvd = dev(kv)
+    block_bytes = 2 * 16 * 8 * 80 * 2
+    past = (_allocation_end(kvd.data_ptr()) - kvd.data_ptr()) // block_bytes
+    assert past >= nb
+    bad = tables.copy()
+    bad[0, 3] = past          # first id whose page ends past the allocation
+    bad[1, 1] = past + 1000
+    # The oracle skips ids >= num_blocks; give it the same skips.
+    want_tables = tables.copy()
+    want_tables[0, 3] = nb + 5
+    want_tables[1, 1] = nb + 5
+    want = O.decode(pool, q, want_tables, ctx, 64)
+    qd = dev(q)
+    out = torch.zeros_like(qd)
+    L = pyvcpp.lib()
+    L.paged_attention_cuda(qd.data_ptr(), kvd.data_ptr(), dev(bad).data_ptr(), ctx.ctypes.data,
+                           out.data_ptr(), 64, 8, 80, 16, 2)
+    torch.cuda.synchronize()
+    assert pyvcpp.last_error() == ""
+    assert_close(out.cpu().numpy(), want, *TOL[O.ORC_F16], what="v1 ids past the allocation")
+
+
 @pytest.mark.parametrize("partition", [0, 32, 128])
 def test_workspace_reuse(cuda, partition):
-    """One zero-initialised workspace across many calls with changing q and
-    pages: the fragment arrival counters must return to zero after each call
-    and no call may see a previous call's partials."""
+    """One workspace across many calls with changing q and pages: no call may
+    see a previous call's partials."""
     nb = 400
     pools = [O.make_pool(O.ORC_F16, 300 + i, nb, 8, 80) for i in range(2)]
     dpools = [DevPool(pl) for pl in pools]

@@ -1,9 +1,12 @@
 """GPU parity of the chunked causal prefill path (vcpp_paged_prefill) against
 the CPU oracle's per-position semantics on identical seeded inputs.
 
-Tolerance (numpy allclose form): atol 2e-3, rtol 1e-2 for fp16, int8 and fp8 pages.
+Tolerance: max-abs error <= 2e-3 and normwise relative error <= 1e-2 for fp16, int8 and fp8
+pages on N(0, 1) data (int8 on the std-2 stress case: 4e-3, see there).
 q is fp16 on the GPU; the oracle gets the same fp16 values as fp32.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -71,7 +74,11 @@ def test_prefill_long_prefix(cuda, kind, D):
                                                      D, std=2.0)
     want = O.prefill(pool, q32, tables, q_start, pre, 16)
     got = gpu_prefill(DevPool(pool), q16, tables, q_start, pre, 16)
-    assert_close(got, want, ATOL, RTOL, what="long prefix D=%d kind=%d" % (D, kind))
+    # int8 V enters the MFMA as fp16(v * scale): one rounding of at most half
+    # an fp16 ulp of the value, so the bound scales with the data (std 2:
+    # twice the N(0, 1) bound).  fp16 and FP8 pages hold V exactly.
+    atol = ATOL * 2.0 if kind == O.ORC_I8 else ATOL
+    assert_close(got, want, atol, RTOL, what="long prefix D=%d kind=%d" % (D, kind))
 
 
 def test_prefill_matches_decode_for_single_token_chunks(cuda):
@@ -87,7 +94,8 @@ def test_prefill_matches_decode_for_single_token_chunks(cuda):
 def test_prefill_config3_sampled(cuda):
     """BASELINE config 3 at full size: 8 chunks x 2048 new tokens on 1024-token
     paged prefixes, 64/8 heads, head_dim 80, fp16 N(0, 0.5); all rows run on
-    the GPU, 96 random rows (and the first/last of each chunk) are checked."""
+    the GPU; 96 random rows (and the first/last of each chunk) and two whole
+    chunks are checked."""
     prefix, chunk = [1024] * 8, [2048] * 8
     pool, q16, q32, tables, q_start, pre = make_case(O.ORC_F16, 640, prefix, chunk, 64, 8,
                                                      std=0.5)
@@ -98,6 +106,12 @@ def test_prefill_config3_sampled(cuda):
                                      q_start[1:] - 1]))
     want = oracle_prefill_rows(pool, q32, tables, q_start, pre, 64, rows)
     assert_close(got[rows], want, ATOL, RTOL, what="config3 rows")
+    # Two whole chunks (the first and the last, 2 x 2048 rows x 64 heads).
+    for c in (0, 7):
+        r0, r1 = int(q_start[c]), int(q_start[c + 1])
+        want_c = O.prefill(pool, q32[r0:r1], tables[c:c + 1], np.array([0, r1 - r0], np.int32),
+                           pre[c:c + 1], 64, nthreads=min(16, os.cpu_count() or 1))
+        assert_close(got[r0:r1], want_c, ATOL, RTOL, what="config3 whole chunk %d" % c)
 
 
 @pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8, O.ORC_FP8])

@@ -7,6 +7,7 @@ selection disabled, and linked into one shared library next to this file.
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -50,11 +51,16 @@ def build(verbose=False, out=LIB, defines=()):
     bdir = os.path.join(HERE, "_build" + tag)
     os.makedirs(bdir, exist_ok=True)
     dflags = ["-D" + d for d in defines]
+    cmds = []
     for src in SOURCES:
         obj = os.path.join(bdir, os.path.basename(src) + ".o")
         lang = ["-x", "hip"]
-        _run([HIPCC] + FLAGS + dflags + lang + ["-c", os.path.join(HERE, src), "-o", obj], verbose)
+        cmds.append([HIPCC] + FLAGS + dflags + lang + ["-c", os.path.join(HERE, src), "-o", obj])
         objs.append(obj)
+    # One hipcc per source, run side by side (each is single-threaded).
+    with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1, 8)) as ex:
+        for f in [ex.submit(_run, c, verbose) for c in cmds]:
+            f.result()
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", out] + objs, verbose)
     return out
 

@@ -36,6 +36,15 @@ int fail(int code, const char* fmt, ...) {
     return code;
 }
 
+}  // namespace
+
+namespace vcpp {
+// Records a failure for vcpp_last_error() from other sources of the library.
+int record_error(int code, const char* msg) { return fail(code, "%s", msg); }
+}  // namespace vcpp
+
+namespace {
+
 bool eps_ok(float eps) { return std::isfinite(eps) && eps >= 0.f; }
 
 int hip_fail(hipError_t e, const char* what) {
@@ -257,6 +266,20 @@ V1State& v1_state() {
     static V1State s;
     return s;
 }
+
+// Whole blocks of block_bytes from base to the end of the device allocation
+// that contains it (INT32_MAX when the runtime does not know the pointer).
+int64_t v1_num_blocks(const void* base, int64_t block_bytes) {
+    if (!base || block_bytes <= 0) return 0;
+    hipDeviceptr_t start = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&start, &size, const_cast<void*>(base)) != hipSuccess || !start) {
+        (void)hipGetLastError();
+        return INT32_MAX;
+    }
+    const int64_t left = (int64_t)((const char*)start + size - (const char*)base);
+    return std::min<int64_t>(left / block_bytes, INT32_MAX);
+}
 }  // namespace
 
 
@@ -462,6 +485,15 @@ void paged_attention_cuda(const float* q, const uint16_t* kv_cache, const int32_
         fail(VCPP_E_INVALID, "paged_attention_cuda: context_lens is NULL");
         return;
     }
+    if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0) {
+        fail(VCPP_E_INVALID, "paged_attention_cuda: num_heads %d is not a positive multiple of "
+             "num_kv_heads %d", num_heads, num_kv_heads);
+        return;
+    }
+    if (head_dim <= 0 || head_dim > 256 || !vcpp::decode_head_dim_supported(VCPP_KV_F16, head_dim)) {
+        fail(VCPP_E_UNSUPPORTED, "paged_attention_cuda: head_dim %d not supported", head_dim);
+        return;
+    }
     // Host read of the lengths, as cuda/attention.cu:25-28 does.
     int32_t max_ctx = 0;
     for (int32_t b = 0; b < batch_size; b++) max_ctx = context_lens[b] > max_ctx ? context_lens[b] : max_ctx;
@@ -472,8 +504,11 @@ void paged_attention_cuda(const float* q, const uint16_t* kv_cache, const int32_
     kv.block_size = block_size;
     kv.num_kv_heads = num_kv_heads;
     kv.head_dim = head_dim;
-    kv.num_blocks = INT32_MAX;  // not passed by v1: block ids are trusted
     const int64_t page = (int64_t)block_size * num_kv_heads * head_dim;
+    // v1 passes no block count: bound block ids by the device allocation that
+    // holds kv_cache (ids whose pages would end past it are skipped, as
+    // get_k skips ids outside the pool, src/kv_cache_manager.cpp:90-95).
+    kv.num_blocks = v1_num_blocks(kv_cache, 2 * page * (int64_t)sizeof(uint16_t));
     kv.block_stride = 2 * page;
     kv.k = kv_cache;
     kv.v = kv_cache ? kv_cache + page : nullptr;

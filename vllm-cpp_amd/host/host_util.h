@@ -8,7 +8,11 @@
 #include <cstdint>
 #include <cstring>
 #include <stdexcept>
+#include <mutex>
 #include <string>
+#include <vector>
+
+#include "vllm_cpp/kv_config.h"
 
 namespace vcpp_host {
 
@@ -71,13 +75,45 @@ inline float f16_decode(uint16_t h) {
     return out;
 }
 
-// A device buffer that only grows.
+// One row [kv_dim] of a pool's page, raw bytes of dtype, to floats exactly as
+// the reference pool decodes it (fp16: src/kv_cache_manager.cpp:120-143;
+// FP8: src/quantization.cpp:25-48); INT8 rows take their [kv_dim / head_dim]
+// fp16 scales.
+inline void decode_row(const uint8_t* raw, const uint16_t* scales, float* out, int32_t kv_dim,
+                       int32_t head_dim, KVDtype dtype) {
+    switch (dtype) {
+        case KVDtype::FP32:
+            std::memcpy(out, raw, sizeof(float) * kv_dim);
+            break;
+        case KVDtype::FP16: {
+            uint16_t h;
+            for (int32_t i = 0; i < kv_dim; ++i) {
+                std::memcpy(&h, raw + 2 * i, 2);
+                out[i] = f16_decode(h);
+            }
+            break;
+        }
+        case KVDtype::FP8_E4M3:
+            for (int32_t i = 0; i < kv_dim; ++i) out[i] = fp8_decode(raw[i]);
+            break;
+        case KVDtype::INT8:
+            for (int32_t i = 0; i < kv_dim; ++i)
+                out[i] = (float)(int8_t)raw[i] * f16_decode(scales[i / head_dim]);
+            break;
+    }
+}
+
+// A device buffer that only grows.  Growing waits for `stream` first: work
+// queued there may still read the old buffer.
 struct DevBuf {
     void* p = nullptr;
     size_t n = 0;
-    void* get(size_t bytes) {
+    void* get(size_t bytes, hipStream_t stream) {
         if (bytes > n) {
-            if (p) (void)hipFree(p);
+            if (p) {
+                check(hipStreamSynchronize(stream), "device scratch: wait before growing");
+                (void)hipFree(p);
+            }
             p = nullptr;
             n = 0;
             check(hipMalloc(&p, bytes), "device scratch allocation");
@@ -91,3 +127,13 @@ struct DevBuf {
 };
 
 }  // namespace vcpp_host
+
+// Device staging of the host entry points (paged_attention.cpp) for one
+// BlockPool: calls on a pool are queued on the pool's stream, so buffers kept
+// per pool are never overwritten by work on another pool's stream.
+struct PoolStaging {
+    std::mutex mu;
+    vcpp_host::DevBuf q, out, tables, ctx, ws, k, v, slots, rows;
+    std::vector<uint8_t> host;  // read_kv_prefill: gathered raw rows
+};
+

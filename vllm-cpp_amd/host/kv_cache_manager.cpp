@@ -54,7 +54,7 @@ void decode_rows(const uint8_t* raw, const uint16_t* scales, float* out, int32_t
 BlockPool::BlockPool(int32_t num_blocks, int32_t num_layers, int32_t kv_dim, KVDtype kv_dtype,
                      int32_t head_dim)
     : kv_dim_(kv_dim), num_layers_(num_layers), kv_dtype_(kv_dtype),
-      head_dim_(head_dim > 0 ? head_dim : kv_dim) {
+      head_dim_(head_dim > 0 ? head_dim : kv_dim), staging_(new PoolStaging()) {
     if (num_blocks < 0 || num_layers <= 0 || kv_dim <= 0 || kv_dim % head_dim_ != 0)
         throw std::invalid_argument("BlockPool: bad shape");
     if (kv_dtype == KVDtype::INT8 && head_dim <= 0)
@@ -84,8 +84,15 @@ BlockPool::BlockPool(int32_t num_blocks, int32_t num_layers, int32_t kv_dim, KVD
 }
 
 BlockPool::~BlockPool() {
+    (void)hipStreamSynchronize(static_cast<hipStream_t>(stream_));
+    staging_.reset();
     for (void* p : {(void*)k_, (void*)v_, (void*)k_scale_, (void*)v_scale_})
         if (p) (void)hipFree(p);
+}
+
+void BlockPool::set_stream(void* stream) {
+    if (stream != stream_) check(hipStreamSynchronize(static_cast<hipStream_t>(stream_)), "set_stream");
+    stream_ = stream;
 }
 
 int32_t BlockPool::alloc() {
