@@ -353,6 +353,7 @@ def cpu_baseline(torch, w, target_s):
         dt += time.perf_counter() - t0
         reps += 1
     out = {"value": reps * w["bytes"] / dt / 1e12, "unit": "TB/s", "cores": cores, "kind": kind,
+           "host_nproc": os.cpu_count(), "host_cores_usable": len(os.sched_getaffinity(0)),
            "sample": "the full config-2 batch (64 seqs, %d context tokens) x %d repetitions, "
                      "paged_attention() per sequence on an FP32 pool holding the decoded fp16 "
                      "values, %.1f s" % (w["total_tokens"], reps, dt)}
@@ -379,8 +380,86 @@ def cpu_port_threaded(torch, w, target_s):
         dt += time.perf_counter() - t0
         reps += 1
     return {"value": reps * w["bytes"] / dt / 1e12, "unit": "TB/s", "cores": cores, "kind": "port",
+            "host_nproc": os.cpu_count(), "host_cores_usable": len(os.sched_getaffinity(0)),
             "sample": "the full config-2 batch x %d repetitions, oracle threaded over (sequence, head), "
                       "%.1f s" % (reps, dt)}
+
+
+def cpu_prefill_sample(torch, pw, target_s):
+    """The reference's prefill on the host (src/paged_engine.cpp:381-384 runs
+    one paged_attention-style pass per position; oracle/_ref's ref_prefill
+    calls paged_attention() per query row with seq_len = prefix + i + 1), one
+    core, on a bounded sample of config 3: rows 0, 16, 32, ... of chunk 0
+    (prefix 1024), an FP32 pool holding the chunk's fp16 K/V values."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    if not O.ref_available():
+        return None
+    tab = pw["tables"][0].long()
+    kf = pw["k"][tab].float().cpu().numpy()   # the chunk's blocks, in table order
+    vf = pw["v"][tab].float().cpu().numpy()
+    pool = O.RefPool(kf, vf, fp16=False)
+    rows = np.arange(0, pw["new"], 16)
+    q = pw["q"][rows].float().cpu().numpy()
+    tables = np.tile(np.arange(kf.shape[0], dtype=np.int32), (len(rows), 1))
+    q_start = np.arange(len(rows) + 1, dtype=np.int32)
+    prefix = (pw["prefix_len"] + rows).astype(np.int32)
+    flops = 4 * D * H * int(sum(int(p) + 1 for p in prefix))
+    reps, dt = 0, 0.0
+    while dt < target_s and reps < 100:
+        t0 = time.perf_counter()
+        pool.prefill(q, tables, q_start, prefix, H)
+        dt += time.perf_counter() - t0
+        reps += 1
+    return {"value": reps * flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "reference",
+            "host_nproc": os.cpu_count(),
+            "sample": "config 3 chunk 0, %d query rows (every 16th of 2048, prefix 1024 + i), "
+                      "paged_attention() per row on an FP32 pool holding the fp16 values, "
+                      "%d repetitions, %.1f s" % (len(rows), reps, dt)}
+
+
+def config1_leg(torch, pyvcpp, target_s):
+    """BASELINE config 1 (1 sequence, ctx 512, fp32 q and K/V, 64/8 heads,
+    head_dim 80, 32 blocks permuted over 64): GPU latency of one
+    vcpp_paged_decode call, and the reference on the host with an FP32 pool
+    and with its FP16 pool as is (src/kv_cache_manager.cpp:186-211 converts a
+    whole block on every key access), one core each."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    pool = O.make_pool(O.ORC_F32, 101, 64, 8, 80)
+    q = O.normal(103, (1, 64, 80))
+    table = O.permutation(107, 64)[:32].reshape(1, 32).astype(np.int32)
+    ctx = np.array([512], np.int32)
+    nbytes = 512 * 2 * HKV * D * 4 + 64 * 80 * 8 + 32 * 4
+    dev = torch.device("cuda:0")
+    k = torch.from_numpy(pool.k).to(dev)
+    v = torch.from_numpy(pool.v).to(dev)
+    pages = pyvcpp.kv_pages(pyvcpp.KV_F32, k, v, BS, HKV, D, 64, BS * HKV * D)
+    qd = torch.from_numpy(q).to(dev)
+    out = torch.empty_like(qd)
+    td = torch.from_numpy(table).to(dev)
+    cd = torch.from_numpy(ctx).to(dev)
+    need = pyvcpp.decode_workspace_size(pages, 1, H, 512, 0)
+    ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=dev)
+    run = lambda: pyvcpp.paged_decode(pages, qd, out, td, cd, 512, H, workspace=ws)
+    dt = timed(torch, run, 500)
+    res = {"workload": "BASELINE config 1: 1 seq, ctx 512, fp32 q / K/V pages, 64 q / 8 kv heads, "
+                       "head_dim 80, 32 blocks over 64", "bytes": nbytes,
+           "gpu_us_per_call": round(dt * 1e6, 2), "gpu_TB/s": round(nbytes / dt / 1e12, 4)}
+    if O.ref_available() and target_s > 0:
+        for name, fp16 in (("cpu_ref_fp32_pool", False), ("cpu_ref_fp16_pool_as_is", True)):
+            rp = O.RefPool(pool.k, pool.v, fp16=fp16)
+            reps, t = 0, 0.0
+            while t < target_s and reps < 100000:
+                t0 = time.perf_counter()
+                rp.decode(q, table, ctx, H)
+                t += time.perf_counter() - t0
+                reps += 1
+            res[name] = {"us_per_call": round(t / reps * 1e6, 1), "TB/s": nbytes * reps / t / 1e12,
+                         "cores": 1, "calls": reps}
+    return res
 
 
 def read_traffic(name):
@@ -662,9 +741,13 @@ def main():
         result["fp8_decode"] = bench_fp8(torch, pyvcpp, args)
         result["kv_write"] = bench_kvwrite(torch, pyvcpp, args)
         result["dense"] = bench_dense(torch, pyvcpp, args)
+    if not args.no_configs:
+        result["config1"] = config1_leg(torch, pyvcpp, 0.0 if args.no_cpu else 2.0)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(torch, w, args.cpu_seconds)
         result["cpu_port_threaded"] = cpu_port_threaded(torch, w, min(args.cpu_seconds, 5.0))
+        if not args.no_prefill:
+            result["cpu_prefill"] = cpu_prefill_sample(torch, prefill_workload(torch, args.seed + 7), 5.0)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result))

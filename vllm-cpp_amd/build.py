@@ -65,6 +65,16 @@ def build(verbose=False, out=LIB, defines=()):
     return out
 
 
+GATHER_LIB = os.path.join(HERE, "libvcpp_attn_gather.so")
+
+
+def build_gather_checker(verbose=False):
+    """libvcpp_attn_gather.so: the same sources with -DVCPP_GATHER_DUMP, whose
+    kernels also record the (block, slot) each (sequence, position) is loaded
+    from (tests/test_gather_gpu.py).  A checker build; the product is LIB."""
+    return build(verbose, out=GATHER_LIB, defines=["VCPP_GATHER_DUMP"])
+
+
 def build_host_test(verbose=False):
     """tests/cpp/host_api_test: the C++ BlockPool / KVCacheManager /
     paged_attention checks, linked against this library and the CPU oracle

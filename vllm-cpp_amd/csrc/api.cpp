@@ -38,6 +38,12 @@ int fail(int code, const char* fmt, ...) {
 
 }  // namespace
 
+#ifdef VCPP_GATHER_DUMP
+// Checker builds: the dump buffer every following decode / prefill launch writes.
+int32_t* g_gather_dump = nullptr;
+int64_t g_gather_stride = 0;
+#endif
+
 namespace vcpp {
 // Records a failure for vcpp_last_error() from other sources of the library.
 int record_error(int code, const char* msg) { return fail(code, "%s", msg); }
@@ -287,6 +293,16 @@ extern "C" {
 
 const char* vcpp_last_error(void) { return g_last_error.c_str(); }
 
+#ifdef VCPP_GATHER_DUMP
+// Checker builds only (not declared in include/): set (or clear, with NULL)
+// the device buffer [rows][stride][2] int32 that decode and prefill launches
+// record their (block, slot) gather indices into.
+void vcpp_debug_gather_dump(int32_t* buf, int64_t stride) {
+    g_gather_dump = buf;
+    g_gather_stride = buf ? stride : 0;
+}
+#endif
+
 const char* vcpp_version(void) { return "vcpp_attn 0.1 gfx950"; }
 
 size_t vcpp_decode_workspace_size(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_heads,
@@ -362,6 +378,10 @@ int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
         p.pipeline = e ? atoi(e) : 0;
     }
     p.scale_log2 = (1.0f / std::sqrt((float)kv->head_dim)) * 1.4426950408889634f;
+#ifdef VCPP_GATHER_DUMP
+    p.gather_dump = g_gather_dump;
+    p.gather_stride = g_gather_stride;
+#endif
     if (p.pairs > 65535 * 8) return fail(VCPP_E_UNSUPPORTED, "too many kv heads");
     hipError_t e = vcpp::launch_decode(p, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "decode launch");
@@ -421,6 +441,10 @@ int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
     p.max_chunk_len = max_chunk_len;
     p.scale_log2 = (1.0f / std::sqrt((float)kv->head_dim)) * 1.4426950408889634f;
     p.bs_magic = ((1ull << 40) + kv->block_size - 1) / kv->block_size;
+#ifdef VCPP_GATHER_DUMP
+    p.gather_dump = g_gather_dump;
+    p.gather_stride = g_gather_stride;
+#endif
     hipError_t e = vcpp::launch_prefill(p, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "prefill launch");
     return VCPP_OK;

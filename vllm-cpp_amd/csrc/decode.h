@@ -53,6 +53,10 @@ struct DecodeParams {
     float scale_log2;  // log2(e) / sqrt(head_dim)
     int32_t pipeline;  // fp16/int8 pipeline shape (tuning; 0 = default)
     int32_t page_mode; // fp16/int8, Hkv 8: one 8-wave workgroup per range staging whole tiles in LDS
+#ifdef VCPP_GATHER_DUMP
+    int32_t* gather_dump;    // checker builds: [rows][gather_stride][2] (block, slot)
+    int64_t gather_stride;
+#endif
 };
 
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);

@@ -462,6 +462,11 @@ void decode_mfma_kernel(DecodeParams p) {
                     const int tt = it * TPS + j;
                     const int bid = tt < ntiles ? __builtin_amdgcn_readlane(my_bid, tt & 63) : -1;
                     const int off = __builtin_amdgcn_readlane(my_off, tt & 63);
+#ifdef VCPP_GATHER_DUMP
+                    const int gpos = (ch + tt) * kTile + lane;
+                    if (pair == 0 && tt < ntiles && lane < kTile && bid >= 0 && gpos < end)
+                        gather_record(p, s, gpos, bid, off + lane);
+#endif
                     load_tile<KV, D>(buf[j], p, bid, off, lofs);
                 }
             };
@@ -702,6 +707,9 @@ __global__ __launch_bounds__(64) void decode_f32_kernel(DecodeParams p) {
             if (id < 0 || (int64_t)id >= p.num_blocks) id = -1;
         }
         float t = -__builtin_inff();
+#ifdef VCPP_GATHER_DUMP
+        if (id >= 0 && head == 0) gather_record(p, seq, pos, id, pos - lb * p.block_size);
+#endif
         if (id >= 0) {
             const float* kr = kb + (int64_t)id * p.block_stride +
                               ((int64_t)(pos - lb * p.block_size) * p.num_kv_heads + kvh) * D;
@@ -958,6 +966,10 @@ void decode_page_kernel(DecodeParams p) {
             const PageEntry& e = list[tau - win0];
             bid = e.bid;
             tok = e.tok;
+#ifdef VCPP_GATHER_DUMP
+            const int gpos = e.tis * kTile + lane;
+            if (wave == 0 && lane < kTile && bid >= 0 && gpos < e.end) gather_record(p, e.seq, gpos, bid, tok + lane);
+#endif
         }
         const int64_t elem = (int64_t)(bid >= 0 ? bid : 0) * p.block_stride + (int64_t)tok * HKV * D;
 #pragma unroll

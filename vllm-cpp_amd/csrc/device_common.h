@@ -104,4 +104,19 @@ __device__ __forceinline__ h4 bytes4_to_h4(uint32_t x) {
 }
 
 
+// Gather-index dump (checker builds only, -DVCPP_GATHER_DUMP): every kernel
+// that addresses K/V pages records, per (sequence or chunk, position), the
+// physical block and slot it loads, into an int32 [rows][stride][2] buffer the
+// test reads back and compares with the block table.
+#ifdef VCPP_GATHER_DUMP
+template <class P>
+__device__ __forceinline__ void gather_record(const P& p, int row, int pos, int bid, int slot) {
+    if (p.gather_dump && pos < p.gather_stride) {
+        int32_t* e = p.gather_dump + 2 * ((int64_t)row * p.gather_stride + pos);
+        e[0] = bid;
+        e[1] = slot;
+    }
+}
+#endif
+
 }  // namespace vcpp

@@ -36,6 +36,10 @@ struct PrefillParams {
     int32_t max_chunk_len;
     float scale_log2;  // log2(e) / sqrt(head_dim)
     uint64_t bs_magic; // ceil(2^40 / block_size): pos / block_size = (pos * bs_magic) >> 40
+#ifdef VCPP_GATHER_DUMP
+    int32_t* gather_dump;    // checker builds: [rows][gather_stride][2] (block, slot)
+    int64_t gather_stride;
+#endif
 };
 
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream);

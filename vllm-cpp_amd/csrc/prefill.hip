@@ -273,6 +273,9 @@ void prefill_dma_kernel(PrefillParams p) {
             const int lb = (int)(((uint64_t)(uint32_t)pos * p.bs_magic) >> 40);
             const int bid = table_s[lb];
             if (bid >= 0) off = bid * page_bytes + (pos - lb * p.block_size) * row_bytes + lane_off;
+#ifdef VCPP_GATHER_DUMP
+            if (bid >= 0 && wave == 0 && kvh == 0 && hg == 0) gather_record(p, chunk, pos, bid, pos - lb * p.block_size);
+#endif
         }
 #pragma unroll
         for (int i = 0; i < PERW; ++i) {
@@ -304,6 +307,9 @@ void prefill_dma_kernel(PrefillParams p) {
                 const int slot = pos - lb * p.block_size;
                 off = bid * p.block_stride + ((int64_t)slot * p.num_kv_heads + kvh) * D;
                 soff = ((int64_t)bid * p.scale_block_stride + (int64_t)kvh * p.block_size + slot) * 2;
+#ifdef VCPP_GATHER_DUMP
+                if (wave == 0 && lane < 32 && kvh == 0 && hg == 0) gather_record(p, chunk, pos, bid, slot);
+#endif
             }
         }
 #pragma unroll
@@ -616,7 +622,10 @@ hipError_t launch_dma(const PrefillParams& p, hipStream_t stream) {
     constexpr int QT = 16 * rows_blocks<KV, D>();
     dim3 grid((p.max_chunk_len + QT - 1) / QT, p.num_chunks,
               p.num_kv_heads * p.head_groups);
-    const size_t lds = prefill_lds_bytes(KV, D, p.max_blocks);
+    size_t lds = prefill_lds_bytes(KV, D, p.max_blocks);
+#ifdef VCPP_PREFILL_LDS_PAD
+    lds = std::max<size_t>(lds, VCPP_PREFILL_LDS_PAD);
+#endif
     // Raise the kernel's dynamic LDS limit on this device only when a launch
     // needs more than it was last set to there (the attribute call is a host
     // round trip; the limit is per device).

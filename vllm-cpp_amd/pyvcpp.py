@@ -78,7 +78,20 @@ def lib():
     if not os.path.exists(LIB_PATH):
         raise RuntimeError(
             "libvcpp_attn.so not built (%s); run __graft_entry__.build()" % LIB_PATH)
-    L = ctypes.CDLL(LIB_PATH)
+    _lib = open_library(LIB_PATH)
+    return _lib
+
+
+GATHER_LIB_PATH = os.path.join(HERE, "libvcpp_attn_gather.so")
+
+
+def open_library(path):
+    """Loads a build of the library at `path` with every entry point's
+    argument types set (lib() loads the product build; tests also open the
+    gather-index checker build, GATHER_LIB_PATH)."""
+    if not os.path.exists(path):
+        raise RuntimeError("%s not built; run __graft_entry__.build()" % path)
+    L = ctypes.CDLL(path)
     L.vcpp_last_error.restype = ctypes.c_char_p
     L.vcpp_version.restype = ctypes.c_char_p
     vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
@@ -112,7 +125,9 @@ def lib():
     L.vcpp_profile_read.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                     ctypes.POINTER(ctypes.c_int64)]
     L.vcpp_profile_read.restype = ctypes.c_int
-    _lib = L
+    if hasattr(L, "vcpp_debug_gather_dump"):
+        L.vcpp_debug_gather_dump.argtypes = [vp, i64]
+        L.vcpp_debug_gather_dump.restype = None
     return L
 
 
