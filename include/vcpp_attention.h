@@ -129,6 +129,26 @@ int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
 size_t vcpp_decode_workspace_size(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_heads,
                                   int32_t max_context_len, int32_t partition_size);
 
+/*
+ * vcpp_paged_decode without a workspace and without allocating: the split-K
+ * partials go to a static device array of VCPP_NOALLOC_SCRATCH_BYTES that the
+ * library holds on every GPU it runs on until the process ends.  No
+ * counterpart in the reference: it is for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Arguments and results as vcpp_paged_decode.  A call whose
+ * partials would need more than the array (vcpp_decode_workspace_size) fails
+ * with VCPP_E_UNSUPPORTED and launches nothing; the balanced split
+ * (partition_size 0) of a 256-CU GPU needs at most ~21 MB at head_dim 80.
+ * Every call on a GPU shares that GPU's array: calls that may overlap on one
+ * GPU (different streams) race; calls on one stream are ordered.
+ */
+#define VCPP_NOALLOC_SCRATCH_BYTES (64u << 20)
+int vcpp_paged_decode_noalloc(const vcpp_kv_pages* kv, const float* q, float* out,
+                              const int32_t* block_tables, int32_t max_blocks_per_seq,
+                              const int32_t* table_lens, const int32_t* context_lens,
+                              int32_t num_seqs, int32_t max_context_len, int32_t num_heads,
+                              int32_t partition_size, void* stream);
+
 /* ---- v2: chunked causal prefill ---------------------------------------- */
 
 /*

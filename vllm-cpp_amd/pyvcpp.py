@@ -28,6 +28,7 @@ EXPORTS = [
     "vcpp_last_error",
     "vcpp_version",
     "vcpp_paged_decode",
+    "vcpp_paged_decode_noalloc",
     "vcpp_decode_workspace_size",
     "vcpp_paged_prefill",
     "vcpp_write_kv",
@@ -98,6 +99,9 @@ def open_library(path):
     L.vcpp_paged_decode.argtypes = [ctypes.POINTER(KVPages), vp, vp, vp, i32, vp, vp, i32, i32,
                                     i32, i32, vp, sz, vp]
     L.vcpp_paged_decode.restype = ctypes.c_int
+    L.vcpp_paged_decode_noalloc.argtypes = [ctypes.POINTER(KVPages), vp, vp, vp, i32, vp, vp, i32,
+                                            i32, i32, i32, vp]
+    L.vcpp_paged_decode_noalloc.restype = ctypes.c_int
     L.vcpp_decode_workspace_size.argtypes = [ctypes.POINTER(KVPages), i32, i32, i32, i32]
     L.vcpp_decode_workspace_size.restype = sz
     L.vcpp_paged_prefill.argtypes = [ctypes.POINTER(KVPages), vp, vp, vp, i32, vp, vp, i32, i32,
@@ -181,6 +185,19 @@ def paged_decode(pages, q, out, block_tables, context_lens, max_context_len, num
                                  max_blocks, _ptr(table_lens), _ptr(context_lens), num_seqs,
                                  max_context_len, num_heads, partition_size, _ptr(workspace),
                                  ws_bytes, _stream(stream))
+    _check(rc)
+    return out
+
+
+def paged_decode_noalloc(pages, q, out, block_tables, context_lens, max_context_len, num_heads,
+                         table_lens=None, partition_size=0, stream=None):
+    """vcpp_paged_decode_noalloc: as paged_decode, with the library's static
+    split-K scratch instead of a workspace (allocates nothing)."""
+    num_seqs = q.shape[0]
+    max_blocks = block_tables.shape[1] if block_tables is not None and block_tables.dim() == 2 else 0
+    rc = lib().vcpp_paged_decode_noalloc(ctypes.byref(pages), _ptr(q), _ptr(out), _ptr(block_tables),
+                                         max_blocks, _ptr(table_lens), _ptr(context_lens), num_seqs,
+                                         max_context_len, num_heads, partition_size, _stream(stream))
     _check(rc)
     return out
 
