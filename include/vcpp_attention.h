@@ -108,9 +108,11 @@ typedef struct vcpp_kv_pages {
  *   partition_size   0 (default): the tiles of all sequences are split
  *                evenly over the workgroups the GPU holds at once (fp16/int8/fp8)
  *                or into 256-token partitions (fp32).  > 0 (a multiple of 16,
- *                <= 1024): about that many tokens per workgroup range or
- *                partition -- a tuning and test knob.  Ranges that end inside a
- *                sequence leave partials, merged by a log-sum-exp kernel.
+ *                <= 1024): fixed partitions -- the tiles are split into
+ *                ranges of about that many tokens (fp16/int8/fp8: walked in
+ *                runs by the resident workgroups) or partitions of exactly
+ *                that many tokens (fp32).  Ranges that end inside a sequence
+ *                leave partials, merged by a log-sum-exp kernel.
  *   workspace    device scratch of at least vcpp_decode_workspace_size(...)
  *                bytes (may be NULL when that size is 0); scratch for the
  *                call only, so calls that may overlap need separate ones.

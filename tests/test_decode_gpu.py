@@ -52,7 +52,8 @@ def test_config1(cuda, kind, partition):
 
 @pytest.mark.parametrize("partition", [64, 0])
 @pytest.mark.parametrize("kind", KINDS)
-@pytest.mark.parametrize("heads", [(1, 1), (8, 1), (64, 8), (12, 4), (32, 2), (32, 8)])
+@pytest.mark.parametrize("heads", [(1, 1), (8, 1), (64, 8), (12, 4), (32, 2), (32, 8), (24, 8),
+                                   (8, 8), (56, 8)])
 def test_small_cases(cuda, kind, heads, partition):
     H, Hkv = heads
     ctx = np.array([0, 1, 15, 16, 17, 33, 100, 257], dtype=np.int32)

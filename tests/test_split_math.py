@@ -104,3 +104,49 @@ def test_split_edge_cases(X):
     check([2048] * 16, X, 256)              # config 4's shape class
     check([1] * 1000, X, 256)               # many one-tile sequences
     check([3000, 1, 1, 1, 4096], X, 512)    # long ones around short ones
+
+
+def span_start(w, T, G, WG):
+    """decode_page_kernel with fixed partitions: workgroup w of WG walks the
+    ranges [range_start(w, G, WG), range_start(w + 1, G, WG)) of the G-range
+    split of T tiles (no switch units)."""
+    return range_start(range_start(w, G, WG), T, G)
+
+
+def span_of(t, T, G, WG):
+    """merge_split_kernel's Spans::span_of."""
+    r = range_of(t, T, G)
+    return r if WG == G else range_of(r, G, WG)
+
+
+def span_live(w, T, G, WG):
+    return T >= G or span_start(w, T, G, WG) < span_start(w + 1, T, G, WG)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_partition_spans(seed):
+    """Fixed partitions on the page kernel: every tile's workgroup as the
+    merge computes it is the workgroup whose span holds the tile, and the
+    spans the merge treats as live are exactly the non-empty ones."""
+    rng = np.random.default_rng(99 + seed)
+    for _ in range(40):
+        T = int(rng.integers(1, 40000))
+        G = int(rng.integers(1, 4096))
+        WG = int(min(G, rng.choice([1, 7, 256, 512, G])))
+        starts = [span_start(w, T, G, WG) for w in range(WG + 1)]
+        assert starts[0] == 0 and starts[-1] == T
+        assert all(a <= b for a, b in zip(starts, starts[1:]))
+        for t in list(rng.integers(0, T, 50)) + [0, T - 1]:
+            w = span_of(int(t), T, G, WG)
+            assert starts[w] <= t < starts[w + 1]
+        for w in range(WG):
+            assert span_live(w, T, G, WG) == (starts[w] < starts[w + 1])
+
+
+def test_partition_spans_config4():
+    """Config 4 at 256-token partitions on 256 workgroups: 2048 partitions of
+    16 tiles, 8 per workgroup, every workgroup span inside one sequence."""
+    T, G, WG = 16 * 2048, 16 * 2048 // 16, 256
+    for w in range(WG):
+        a, b = span_start(w, T, G, WG), span_start(w + 1, T, G, WG)
+        assert b - a == 128 and a // 2048 == (b - 1) // 2048

@@ -94,7 +94,8 @@ int device_cus() {
 // Launch geometry and workspace layout of one decode call.
 struct DecodePlan {
     int32_t num_wg = 0;      // fp16/int8: workgroup ranges per kv-head group
-    bool page_mode = false;  // fp16/int8, Hkv 8: page-staged kernel, one workgroup per range
+    bool page_mode = false;  // fp16/int8, Hkv 8: page-staged kernel
+    int32_t page_grid = 0;   // page mode: workgroups (one per range, or a run of ranges each)
     int32_t partition = 0;   // fp32: tokens per partition
     int32_t max_parts = 0;   // fp32: partitions per sequence
     size_t off_o = 0, off_ml = 0, bytes = 0;
@@ -131,7 +132,7 @@ DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_he
          (kv->dtype != VCPP_KV_I8 ||
           (kv->scale_block_stride % 8 == 0 && reinterpret_cast<uintptr_t>(kv->k_scale) % 16 == 0 &&
            reinterpret_cast<uintptr_t>(kv->v_scale) % 16 == 0)));
-    pl.page_mode = partition_size == 0 && !(pe && pe[0] == '0') && dma_aligned &&
+    pl.page_mode = !(pe && pe[0] == '0') && dma_aligned &&
                    vcpp::decode_page_mode_supported(kv->dtype, kv->num_kv_heads, group, D,
                                                     kv->block_size);
     // Ranges that are all resident at once: 2 waves per SIMD, 4 SIMDs per CU
@@ -147,6 +148,12 @@ DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_he
     }
     G = std::max<int64_t>(1, std::min<int64_t>(G, kMaxRanges));
     pl.num_wg = (int32_t)G;
+    // Page mode: the balanced split has one resident workgroup per range;
+    // fixed partitions (more ranges than fit at once) are walked by that many
+    // workgroups, each taking a contiguous run of ranges.
+    pl.page_grid = pl.page_mode ? (int32_t)std::min<int64_t>(
+                                      G, (int64_t)device_cus() * vcpp::decode_page_wg_per_cu(kv->dtype))
+                                : pl.num_wg;
     pl.off_o = 0;
     const size_t blocks = (size_t)G * 2 * pairs;  // [range][slot][kv-head slot]
     pl.off_ml = pl.off_o + align256(blocks * 8 * D * sizeof(float));
@@ -367,7 +374,10 @@ int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
     p.max_parts = pl.max_parts;
     p.num_wg = pl.num_wg;
     p.page_mode = pl.page_mode ? 1 : 0;
-    p.switch_tiles = pl.page_mode ? kSwitchTiles : 0;
+    p.page_grid = pl.page_grid;
+    // Switch units only for the balanced page split (the merge kernel maps
+    // tiles to ranges on the same axis).
+    p.switch_tiles = pl.page_mode && partition_size == 0 ? kSwitchTiles : 0;
     p.ctx_cap = max_context_len;
     if (need > 0) {
         p.ws_o = reinterpret_cast<float*>(ws + pl.off_o);

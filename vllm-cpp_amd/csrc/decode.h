@@ -52,7 +52,8 @@ struct DecodeParams {
     float2* ws_ml;   // (max in log2 units, sum of exponentials)
     float scale_log2;  // log2(e) / sqrt(head_dim)
     int32_t pipeline;  // fp16/int8 pipeline shape (tuning; 0 = default)
-    int32_t page_mode; // fp16/int8, Hkv 8: one 8-wave workgroup per range staging whole tiles in LDS
+    int32_t page_mode; // fp16/int8, Hkv 8: 8-wave workgroups staging whole tiles in LDS
+    int32_t page_grid; // workgroups that walk the num_wg ranges (page mode: a run each; else num_wg)
 #ifdef VCPP_GATHER_DUMP
     int32_t* gather_dump;    // checker builds: [rows][gather_stride][2] (block, slot)
     int64_t gather_stride;

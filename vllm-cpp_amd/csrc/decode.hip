@@ -8,9 +8,9 @@
 //
 // fp16 / int8 / FP8 pages (the HBM-bound path) run one of two kernels with the
 // same split, MFMA step and merge (below).
-//  * decode_page_kernel -- Hkv = 8, <= 8 query heads per kv head, D 64 or 80,
-//    balanced split: a workgroup of 8 waves (one per kv head) walks its range
-//    of 16-token tiles.  Each tile's K rows and V rows (16 tokens x all kv
+//  * decode_page_kernel -- Hkv = 8, <= 8 query heads per kv head, D 64 or 80:
+//    a workgroup of 8 waves (one per kv head) walks its range of 16-token
+//    tiles (balanced split), or a run of fixed-partition ranges.  Each tile's K rows and V rows (16 tokens x all kv
 //    heads: one contiguous run of the page each) are DMA'd into an LDS ring
 //    with global_load_lds_dwordx4 (1 KiB of whole lines per instruction,
 //    explicit vmcnt bookkeeping), chunk order XOR-swizzled by token, one
@@ -18,7 +18,7 @@
 //    pages: a 3-tile ring per workgroup and two workgroups per CU; K widened
 //    in registers, V read transposed straight from the byte tile with
 //    ds_read_b64_tr_b8, int8 scales in one more DMA instruction per tile.
-//  * decode_mfma_kernel -- every other shape, and fixed partitions: one wave
+//  * decode_mfma_kernel -- every other shape: one wave
 //    per (kv head, chunk of <= 8 query heads of its GQA group); workgroups hold
 //    4 waves = 4 kv heads = 640 contiguous bytes of each token row.  Its loads
 //    are described at the end of this comment.
@@ -292,13 +292,27 @@ __device__ __forceinline__ int64_t frag_block(int w0, int i, int pairs, int pair
 // Lane (i8, h) = (lane / 8, lane % 8) owns fragment weights; output element
 // e = lane + 64 k (head e / D) of the 8 x D block is lane-owned.  `wts` is the
 // wave's LDS scratch (>= 80 floats).
+// Workgroup spans of the split axis (Tv tiles, G ranges walked by WG
+// workgroups, WG <= G): workgroup w covers ranges [range_start(w, G, WG),
+// range_start(w + 1, G, WG)).  With WG == G a span is one range.
+struct Spans {
+    int Tv, G, WG;
+    __device__ int start(int w) const { return range_start(range_start(w, G, WG), Tv, G); }
+    __device__ int span_of(int t) const {
+        const int r = range_of(t, Tv, G);
+        return WG == G ? r : range_of(r, G, WG);
+    }
+    // Every span holds a tile when every range does (Tv >= G, WG <= G).
+    __device__ bool live(int w) const { return Tv >= G || start(w) < start(w + 1); }
+};
+
 template <int D>
 __device__ __forceinline__ void merge_fragments(const DecodeParams& p, int s, int w0, int w1,
-                                                int pair, int head_base, int gc, int T, int lane,
+                                                int pair, int head_base, int gc, const Spans& sp,
+                                                int lane,
                                                 __attribute__((address_space(3))) float* wts) {
     // output element e = 4 lane + 256 k4 (.. +3, all in head e / D since D % 4 == 0)
     constexpr int K4 = (8 * D + 255) / 256;
-    const int G = p.num_wg;
     const int nfr = w1 - w0 + 1;
     const int i8 = lane >> 3, h = lane & 7;
     const int n_out = gc * D;
@@ -312,7 +326,7 @@ __device__ __forceinline__ void merge_fragments(const DecodeParams& p, int s, in
         float2 ml = make_float2(kMaxSeed, 0.f);
         {
             const int i = i0 + i8;
-            const bool ok = i < nfr && h < gc && range_live(w0 + i, T, G);
+            const bool ok = i < nfr && h < gc && sp.live(w0 + i);
             const int64_t idx = frag_block(w0, ok ? i : 0, p.pairs, pair) * 16 + h;
             const float2 x = __builtin_bit_cast(
                 float2, __builtin_amdgcn_raw_buffer_load_b64(mlr, (int)(idx * 8), 0, 0));
@@ -323,7 +337,7 @@ __device__ __forceinline__ void merge_fragments(const DecodeParams& p, int s, in
         for (int j = 0; j < 8; ++j) {
             // an empty or missing fragment reads fragment 0 (weight 0 below)
             const int i = i0 + j;
-            const bool ok = i < nfr && range_live(w0 + i, T, G);
+            const bool ok = i < nfr && sp.live(w0 + i);
             const float* row = p.ws_o + frag_block(w0, ok ? i : 0, p.pairs, pair) * (8 * D);
             const auto rr = make_rsrc(row, n_out * 4);
 #pragma unroll
@@ -661,10 +675,11 @@ __global__ __launch_bounds__(256) void merge_split_kernel(DecodeParams p) {
     if (E <= S) return;  // no tiles: zeroed by the decode kernel
     // the split's axis: tile t of s sits at t + X (non-empty sequences up to s)
     const int Tv = T + X * K, shift = X * (KS + 1);
-    const int w0 = range_of(S + shift, Tv, G), w1 = range_of(E - 1 + shift, Tv, G);
+    const Spans sp{Tv, G, p.page_grid};
+    const int w0 = sp.span_of(S + shift), w1 = sp.span_of(E - 1 + shift);
     if (w0 == w1) return;  // finished in place
     const int kvh = pair / p.qchunks, qc = pair - kvh * p.qchunks;
-    merge_fragments<D>(p, s, w0, w1, pair, kvh * p.group + qc * 8, min(8, p.group - qc * 8), Tv,
+    merge_fragments<D>(p, s, w0, w1, pair, kvh * p.group + qc * 8, min(8, p.group - qc * 8), sp,
                        lane, reinterpret_cast<__attribute__((address_space(3))) float*>(
                                  (__attribute__((address_space(3))) float*)wts_all[wave]));
 }
@@ -895,7 +910,14 @@ void decode_page_kernel(DecodeParams p) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
-    const int w = blockIdx.x, G = p.num_wg;
+    // Ranges of the split: G in all.  Workgroup w walks the contiguous ranges
+    // [r_lo, r_hi) with one DMA ring: one range for the balanced split; with
+    // fixed partitions (G > workgroups, no switch units) a run of whole
+    // partitions, whose online softmax combines them in registers.  Either
+    // way a workgroup leaves at most one fragment per sequence end, indexed
+    // by the workgroup (span_of in the merge kernel).
+    const int G = p.num_wg, WG = gridDim.x;
+    const int r_lo = range_start(blockIdx.x, G, WG), r_hi = range_start(blockIdx.x + 1, G, WG);
     const int kvh = wave, pair = wave;  // group <= 8: one query chunk per kv head
     const int head_base = kvh * p.group;
     const int gc = p.group;
@@ -933,8 +955,8 @@ void decode_page_kernel(DecodeParams p) {
         }
         return T;
     };
-    const int a = real_of(range_start(w, Tv, G)), b = real_of(range_start(w + 1, Tv, G));
-    const bool zero_owner_tail = (T == 0 && w == 0) || (T > 0 && w == G - 1);
+    const int a = real_of(range_start(r_lo, Tv, G)), b = real_of(range_start(r_hi, Tv, G));
+    const bool zero_owner_tail = (T == 0 && blockIdx.x == 0) || (T > 0 && (int)blockIdx.x == WG - 1);
 
     // Zero the outputs of empty sequences this range owns (wave 0).
     if (wave == 0) {
@@ -1031,25 +1053,26 @@ void decode_page_kernel(DecodeParams p) {
         const bool odd = (c & 1) != 0;
         const int rr = odd ? rk1 : rk0;
         const int h = 4 * (g & 1) + rr;
-        const int64_t blk = ((int64_t)w * 2 + slot) * p.pairs + pair;
+        const int64_t blk = ((int64_t)blockIdx.x * 2 + slot) * p.pairs + pair;
         float* orow = complete ? p.out + ((int64_t)cur * p.num_heads + head_base + h) * D
                                : p.ws_o + (blk * 8 + h) * D;
         float lsel = lh[0];
 #pragma unroll
         for (int r = 1; r < 4; ++r) lsel = rr == r ? lh[r] : lsel;
         const float scl = complete ? 1.0f / (lsel + 1e-9f) : 1.0f;
-        if (h < gc) {
+        // The swap runs on every lane: with an odd group size the partner of
+        // the last even head's lane stores nothing but must still supply its
+        // value.
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                float x0 = o[t][0], x1 = o[t][1];
-                if (rk0 == 2) {
-                    x0 = o[t][2];
-                    x1 = o[t][3];
-                }
-                const float y = dpp_swap1(odd ? x0 : x1);  // neighbour in the pair
-                const float2 v = odd ? make_float2(y * scl, x1 * scl) : make_float2(x0 * scl, y * scl);
-                *reinterpret_cast<float2*>(orow + 16 * t + (c & ~1)) = v;
+        for (int t = 0; t < NT; ++t) {
+            float x0 = o[t][0], x1 = o[t][1];
+            if (rk0 == 2) {
+                x0 = o[t][2];
+                x1 = o[t][3];
             }
+            const float y = dpp_swap1(odd ? x0 : x1);  // neighbour in the pair
+            const float2 v = odd ? make_float2(y * scl, x1 * scl) : make_float2(x0 * scl, y * scl);
+            if (h < gc) *reinterpret_cast<float2*>(orow + 16 * t + (c & ~1)) = v;
         }
         // (m, l) of the partial: lanes c < 4 of the first two groups, row 4 g + c
         if (!complete && g < 2 && c < 4 && 4 * g + c < gc) {
@@ -1335,7 +1358,7 @@ hipError_t launch_page(const DecodeParams& p, hipStream_t stream) {
         if (e != hipSuccess) return e;
         if (dev >= 0 && dev < 64) attr_set[dev] = true;
     }
-    hipLaunchKernelGGL((decode_page_kernel<KV, D>), dim3(p.num_wg), dim3(kPageWaves * 64), lds, stream, p);
+    hipLaunchKernelGGL((decode_page_kernel<KV, D>), dim3(p.page_grid), dim3(kPageWaves * 64), lds, stream, p);
     return hipGetLastError();
 }
 
