@@ -392,7 +392,10 @@ int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
     p.gather_dump = g_gather_dump;
     p.gather_stride = g_gather_stride;
 #endif
-    if (p.pairs > 65535 * 8) return fail(VCPP_E_UNSUPPORTED, "too many kv heads");
+    if (p.pairs > (kv->dtype == VCPP_KV_F32 ? 65535 : 65535 * 8))
+        return fail(VCPP_E_UNSUPPORTED, "too many kv heads");
+    if (kv->dtype == VCPP_KV_F32 && num_seqs > 65535)
+        return fail(VCPP_E_UNSUPPORTED, "fp32 pages: too many sequences (%d)", num_seqs);
     hipError_t e = vcpp::launch_decode(p, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "decode launch");
     return VCPP_OK;

@@ -688,80 +688,153 @@ __global__ __launch_bounds__(256) void merge_split_kernel(DecodeParams p) {
 
 // Plain VALU kernel, one wave per (partition, sequence, head).  Logits of the
 // partition live in LDS; the exp2/log2-scaled partials match the merge below.
-__global__ __launch_bounds__(64) void decode_f32_kernel(DecodeParams p) {
-    __shared__ float sl[1024];
-    extern __shared__ float qs_dyn[];
-    const int lane = threadIdx.x;
-    const int seq = blockIdx.y, part = blockIdx.x, head = blockIdx.z;
+// fp32 pages: one workgroup per (partition, sequence, kv head, chunk of up to
+// 8 query heads of its group).  The partition's positions go through LDS in
+// 32-token tiles: the workgroup gathers a tile's K and V rows of its kv head
+// (16-byte lanes, through the block table) once for all of its query heads;
+// thread (head h, token j) forms one score (a D-long dot in fp32, in order),
+// the heads' running max / sum move per tile, and thread (h, dims d, d + 32,
+// ..) accumulates the weighted V rows.  Partitions of a sequence leave
+// (m, l, o) partials for merge_parts_kernel when there are several.
+constexpr int kF32Tile = 32;
+constexpr int kF32Heads = 8;
+
+__global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
+    extern __shared__ __attribute__((aligned(16))) float f32_lds[];
     const int D = p.head_dim;
+    const int tid = threadIdx.x;
+    const int seq = blockIdx.y, part = blockIdx.x;
+    const int kvh = blockIdx.z / p.qchunks, qc = blockIdx.z - kvh * p.qchunks;
+    const int h0 = kvh * p.group + qc * kF32Heads;             // first query head
+    const int nh = min(kF32Heads, p.group - qc * kF32Heads);   // query heads here
     const int ctx = min(p.context_lens[seq], p.max_parts * p.partition);
     const int P = p.partition;
     const int np = ctx <= 0 ? 1 : min((ctx + P - 1) / P, p.max_parts);
-    if (part >= np) return;
-    const int kvh = head / p.group;
+    if (part >= np) return;  // whole workgroup
     int tlen = p.max_blocks;
     if (p.table_lens) tlen = min(tlen, p.table_lens[seq]);
     const int start = part * P;
-    const int stop = min(start + P, ctx);
-    const int end = (int)min((int64_t)stop, (int64_t)tlen * p.block_size);
-    const int n = stop > start ? stop - start : 0;
+    const int stop = max(min(start + P, ctx), start);
+    const int end = (int)min((int64_t)stop, (int64_t)tlen * p.block_size);  // usable positions
 
-    const float* qrow = p.q + ((int64_t)seq * p.num_heads + head) * D;
-    for (int d = lane; d < D; d += 64) qs_dyn[d] = qrow[d];
-    __syncthreads();
-
-    const float* kb = reinterpret_cast<const float*>(p.k);
-    const float* vb = reinterpret_cast<const float*>(p.v);
-    float mx = kMaxSeed;
-    for (int i = lane; i < n; i += 64) {
-        const int pos = start + i;
-        const int lb = pos / p.block_size;
-        int id = -1;
-        if (pos < end) {
-            id = p.block_tables[(int64_t)seq * p.max_blocks + lb];
-            if (id < 0 || (int64_t)id >= p.num_blocks) id = -1;
-        }
-        float t = -__builtin_inff();
+    // LDS: q [8][D], K tile [32][D + 1], V tile [32][D], P [8][32], per-head (m, l, alpha)
+    const int KP = D + 1;  // K row pitch (odd: the 32 rows of a dot fall on distinct banks)
+    float* qs = f32_lds;
+    float* ks = qs + kF32Heads * D;
+    float* vs = ks + kF32Tile * KP;
+    float* ps = vs + kF32Tile * D;
+    float* st = ps + kF32Heads * kF32Tile;  // [8] m, [8] l, [8] alpha
+    for (int e = tid; e < nh * D; e += 256)
+        qs[e] = p.q[((int64_t)seq * p.num_heads + h0) * D + e];
+    if (tid < kF32Heads) {
+        st[tid] = kMaxSeed;
+        st[8 + tid] = 0.f;
+    }
+    // output ownership: thread (h = tid / 32, d = tid % 32 + 32 k)
+    const int oh = tid >> 5, od = tid & 31;
+    float acc[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc[k] = 0.f;
+    const float* kbase = reinterpret_cast<const float*>(p.k);
+    const float* vbase = reinterpret_cast<const float*>(p.v);
+    const int chunks = D / 4;  // 16-byte pieces of a row
+    for (int t0 = start; t0 < stop; t0 += kF32Tile) {
+        __syncthreads();  // previous tile's K, V, P no longer read
+        // gather: piece (row j, chunk c4) of K and V
+        for (int e = tid; e < kF32Tile * chunks; e += 256) {
+            const int j = e / chunks, c4 = e - j * chunks;
+            const int pos = t0 + j;
+            float4 kx = make_float4(0.f, 0.f, 0.f, 0.f), vx = kx;
+            if (pos < end) {
+                const int lb = pos / p.block_size;
+                const int id = p.block_tables[(int64_t)seq * p.max_blocks + lb];
+                if (id >= 0 && (int64_t)id < p.num_blocks) {
+                    const int64_t off = (int64_t)id * p.block_stride +
+                                        ((int64_t)(pos - lb * p.block_size) * p.num_kv_heads + kvh) * D + 4 * c4;
+                    kx = *reinterpret_cast<const float4*>(kbase + off);
+                    vx = *reinterpret_cast<const float4*>(vbase + off);
 #ifdef VCPP_GATHER_DUMP
-        if (id >= 0 && head == 0) gather_record(p, seq, pos, id, pos - lb * p.block_size);
+                    if (c4 == 0 && blockIdx.z == 0) gather_record(p, seq, pos, id, pos - lb * p.block_size);
 #endif
-        if (id >= 0) {
-            const float* kr = kb + (int64_t)id * p.block_stride +
-                              ((int64_t)(pos - lb * p.block_size) * p.num_kv_heads + kvh) * D;
-            float acc = 0.f;
-            for (int d = 0; d < D; ++d) acc = fmaf(qs_dyn[d], kr[d], acc);
-            t = acc * p.scale_log2;
+                }
+            }
+            float* kr = ks + j * KP + 4 * c4;
+            kr[0] = kx.x;
+            kr[1] = kx.y;
+            kr[2] = kx.z;
+            kr[3] = kx.w;
+            *reinterpret_cast<float4*>(vs + j * D + 4 * c4) = vx;
         }
-        sl[i] = t;
-        mx = fmaxf(mx, t);
+        __syncthreads();
+        // scores: thread (head h = tid / 32, token j = tid % 32), skipped
+        // positions -inf; then the head's new max (a 32-lane reduction)
+        {
+            const int h = tid >> 5, j = tid & 31;
+            const int pos = t0 + j;
+            float s = -__builtin_inff();
+            bool ok = h < nh && pos < end;
+            if (ok) {
+                const int lb = pos / p.block_size;
+                const int id = p.block_tables[(int64_t)seq * p.max_blocks + lb];
+                ok = id >= 0 && (int64_t)id < p.num_blocks;
+            }
+            if (ok) {
+                const float* qr = qs + h * D;
+                const float* kr = ks + j * KP;
+                float a = 0.f;
+                for (int d = 0; d < D; ++d) a = fmaf(qr[d], kr[d], a);
+                s = a * p.scale_log2;
+            }
+            float mx = s;
+#pragma unroll
+            for (int k = 16; k >= 1; k >>= 1) mx = fmaxf(mx, shfl_xor(mx, k));
+            const float m_old = st[h];
+            const float m_new = fmaxf(m_old, mx);
+            const float e = ok ? fast_exp2(s - m_new) : 0.f;
+            ps[h * kF32Tile + j] = e;
+            float sum = e;
+#pragma unroll
+            for (int k = 16; k >= 1; k >>= 1) sum += shfl_xor(sum, k);
+            __syncthreads();  // every lane of the head read st[h] before it moves
+            if (j == 0) {
+                const float alpha = fast_exp2(m_old - m_new);
+                st[h] = m_new;
+                st[8 + h] = st[8 + h] * alpha + sum;
+                st[16 + h] = alpha;
+            }
+        }
+        __syncthreads();
+        // outputs: rescale, then the tile's weighted V rows
+        if (oh < nh) {
+            const float alpha = st[16 + oh];
+            const float* pr = ps + oh * kF32Tile;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int d = od + 32 * k;
+                if (d < D) {
+                    float a = acc[k] * alpha;
+                    for (int j = 0; j < kF32Tile; ++j) a = fmaf(pr[j], vs[j * D + d], a);
+                    acc[k] = a;
+                }
+            }
+        }
     }
-    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, shfl_xor(mx, m));
-    float l = 0.f;
-    for (int i = lane; i < n; i += 64) {
-        const float e = fast_exp2(sl[i] - mx);
-        sl[i] = e;
-        l += e;
-    }
-    for (int m = 32; m >= 1; m >>= 1) l += shfl_xor(l, m);
     __syncthreads();
-    for (int d = lane; d < D; d += 64) {
-        float acc = 0.f;
-        for (int i = 0; i < n; ++i) {
-            const float wt = sl[i];
-            if (wt == 0.f) continue;
-            const int pos = start + i;
-            const int lb = pos / p.block_size;
-            const int id = p.block_tables[(int64_t)seq * p.max_blocks + lb];
-            const float* vr = vb + (int64_t)id * p.block_stride +
-                              ((int64_t)(pos - lb * p.block_size) * p.num_kv_heads + kvh) * D;
-            acc = fmaf(wt, vr[d], acc);
-        }
+    if (oh < nh) {
+        const int head = h0 + oh;
+        const float m = st[oh], l = st[8 + oh];
         if (np == 1) {
-            p.out[((int64_t)seq * p.num_heads + head) * D + d] = acc / (l + 1e-9f);
+            const float inv = 1.0f / (l + 1e-9f);
+            float* orow = p.out + ((int64_t)seq * p.num_heads + head) * D;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (od + 32 * k < D) orow[od + 32 * k] = acc[k] * inv;
         } else {
             const int64_t idx = ((int64_t)seq * p.max_parts + part) * p.num_heads + head;
-            p.ws_o[idx * D + d] = acc;
-            if (d == lane && lane == 0) p.ws_ml[idx] = make_float2(mx, l);
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (od + 32 * k < D) p.ws_o[idx * D + od + 32 * k] = acc[k];
+            if (od == 0) p.ws_ml[idx] = make_float2(m, l);
         }
     }
 }
@@ -1399,9 +1472,23 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
     const bool prof = prof_enabled();
     if (p.kv_dtype == VCPP_KV_F32) {
         if (prof) prof_begin(kKernelDecode, stream);
-        dim3 grid(p.max_parts, p.num_seqs, p.num_heads);
-        hipLaunchKernelGGL(decode_f32_kernel, grid, dim3(64), p.head_dim * sizeof(float), stream,
-                           p);
+        const int qchunks = (p.group + kF32Heads - 1) / kF32Heads;
+        dim3 grid(p.max_parts, p.num_seqs, p.num_kv_heads * qchunks);
+        DecodeParams pf = p;
+        pf.qchunks = qchunks;
+        const size_t lds = sizeof(float) * ((size_t)kF32Heads * p.head_dim + (size_t)kF32Tile * (p.head_dim + 1) +
+                                            (size_t)kF32Tile * p.head_dim + kF32Heads * kF32Tile + 24);
+        if (lds > 65536) {  // head_dim > 128: raise the kernel's dynamic LDS limit (per device)
+            static bool attr_set[64] = {};
+            int dev = 0;
+            if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || !attr_set[dev]) {
+                const hipError_t e = hipFuncSetAttribute((const void*)decode_f32_kernel,
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+                if (e != hipSuccess) return e;
+                if (dev >= 0 && dev < 64) attr_set[dev] = true;
+            }
+        }
+        hipLaunchKernelGGL(decode_f32_kernel, grid, dim3(256), lds, stream, pf);
         err = hipGetLastError();
         if (err != hipSuccess) return err;
         if (prof) prof_end(kKernelDecode, stream);
