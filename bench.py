@@ -50,7 +50,9 @@ def parse():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the config 4 (long context) and config 5 (int8 mixed) legs")
     ap.add_argument("--config-steps", type=int, default=20)
-    ap.add_argument("--only", choices=["decode", "prefill", "config4", "config5", "qkprep", "fp8",
+    ap.add_argument("--c4-partitions", type=lambda x: [int(v) for v in x.split(",")],
+                    default=[256, 0], help="config 4 variants: partition sizes (0 = balanced)")
+    ap.add_argument("--only", choices=["decode", "prefill", "config1", "config4", "config5", "qkprep", "fp8",
                                        "kvwrite", "dense"],
                     help="run one leg only and print its JSON (for profiling)")
     ap.add_argument("--prefill-only", action="store_true",
@@ -227,7 +229,7 @@ def bench_config4(torch, pyvcpp, args):
     ctx_d = ctx.to(dev)
     nbytes = int(ctx.sum()) * 2 * HKV * D * 2 + 16 * H * D * 8 + sum(nblk) * 4
     res = {}
-    for part in (256, 0):
+    for part in args.c4_partitions:
         need = pyvcpp.decode_workspace_size(sets[0][0], 16, H, 32768, part)
         ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=dev)
         i = [0]
@@ -254,7 +256,8 @@ def bench_config4(torch, pyvcpp, args):
             "config": {"workload": "BASELINE config 4: 16 seqs x 32768 ctx, 64 q / 8 kv heads, "
                                    "head_dim 80, fp16 pages scattered over a 1.25x pool",
                        "bytes_per_step": nbytes},
-            "value": res["balanced"]["TB/s"], "variants": res, "steps": args.config_steps}
+            "value": res["balanced"]["TB/s"] if "balanced" in res else None, "variants": res,
+            "steps": args.config_steps}
 
 
 def bench_config5(torch, pyvcpp, args):
@@ -658,6 +661,9 @@ def main():
         return
     if args.prefill_only or args.only == "prefill":
         print(json.dumps(bench_prefill(torch, pyvcpp, args)))
+        return
+    if args.only == "config1":
+        print(json.dumps(config1_leg(torch, pyvcpp, 0.0)))
         return
     if args.only == "config4":
         print(json.dumps(bench_config4(torch, pyvcpp, args)))

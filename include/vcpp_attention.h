@@ -107,7 +107,8 @@ typedef struct vcpp_kv_pages {
  *                positions past max_context_len are not attended)
  *   partition_size   0 (default): the tiles of all sequences are split
  *                evenly over the workgroups the GPU holds at once (fp16/int8/fp8)
- *                or into 256-token partitions (fp32).  > 0 (a multiple of 16,
+ *                or (fp32) into partitions of 32..256 tokens sized so the
+ *                workgroups fill the GPU about twice.  > 0 (a multiple of 16,
  *                <= 1024): fixed partitions -- the tiles are split into
  *                ranges of about that many tokens (fp16/int8/fp8: walked in
  *                runs by the resident workgroups) or partitions of exactly

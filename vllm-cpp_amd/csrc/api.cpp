@@ -106,7 +106,15 @@ DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_he
     DecodePlan pl;
     const int D = kv->head_dim;
     if (kv->dtype == VCPP_KV_F32) {
-        pl.partition = partition_size > 0 ? partition_size : kDefaultPartition;
+        // Default: partitions of 32..256 tokens, so that the workgroups
+        // (partition, sequence, kv head, 8-head chunk) fill about two per CU.
+        int32_t dflt = kDefaultPartition;
+        if (partition_size == 0 && max_context_len > 0 && kv->num_kv_heads > 0 && num_heads > 0) {
+            const int64_t chunks = (int64_t)kv->num_kv_heads * ((num_heads / kv->num_kv_heads + 7) / 8);
+            const int64_t want = (int64_t)max_context_len * num_seqs * chunks / (2 * (int64_t)device_cus());
+            dflt = (int32_t)std::min<int64_t>(kDefaultPartition, std::max<int64_t>(32, (want + 31) / 32 * 32));
+        }
+        pl.partition = partition_size > 0 ? partition_size : dflt;
         pl.max_parts = num_parts(max_context_len, pl.partition);
         if (pl.max_parts > 1) {
             const size_t rows = (size_t)num_seqs * pl.max_parts * num_heads;
