@@ -281,3 +281,24 @@ def test_fp8_other_head_dims(cuda, D, partition):
     want = O.decode(pool, q, tables, ctx, 64)
     got = gpu_decode(DevPool(pool), q, tables, ctx, 64, partition_size=partition)
     assert_close(got, want, *TOL[O.ORC_FP8], what="fp8 D=%d P=%d" % (D, partition))
+
+
+@pytest.mark.parametrize("partition", [0, 64])
+@pytest.mark.parametrize("D", [64, 80, 128])
+@pytest.mark.parametrize("heads", [(64, 8), (32, 4), (16, 4), (24, 8)])
+@pytest.mark.parametrize("kind", [O.ORC_F16, O.ORC_I8, O.ORC_FP8])
+def test_page_kernel_shapes(cuda, kind, heads, D, partition):
+    """Every page-staged kernel shape (8 kv heads per workgroup at head_dim 64
+    and 80; 4 per workgroup for 4-head multiples and head_dim 128, walked as
+    head groups of one range) on ragged contexts, both split modes."""
+    H, Hkv = heads
+    ctx = np.array([0, 5, 16, 31, 300, 1025, 777, 64, 2000, 1], dtype=np.int32)
+    nb = int(sum((int(c) + O.BS - 1) // O.BS for c in ctx)) + 6
+    pool = O.make_pool(kind, 3000 + D + H, nb, Hkv, D)
+    q = O.normal(3100 + D + H, (len(ctx), H, D))
+    tables = random_tables(3200 + D, ctx, nb)
+    want = O.decode(pool, q, tables, ctx, H)
+    got = gpu_decode(DevPool(pool), q, tables, ctx, H, partition_size=partition)
+    assert_close(got, want, *TOL[kind], what="page shapes kind=%d H=%d Hkv=%d D=%d P=%d"
+                 % (kind, H, Hkv, D, partition))
+    assert np.all(got[0] == 0.0), "ctx=0 must give zeros"

@@ -147,7 +147,12 @@ DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_he
     // (page mode: 8-wave workgroups that each cover every kv head, one per CU
     // for fp16 pages and two for byte pages).
     const int64_t slots = (int64_t)device_cus() * (8 / wpw);
-    int64_t G = pl.page_mode ? (int64_t)device_cus() * vcpp::decode_page_wg_per_cu(kv->dtype) : slots / groups;
+    // Page mode: each range is walked by num_kv_heads / HW workgroups (one per
+    // head group), so ranges = resident workgroups / head groups.
+    const int page_hw = vcpp::decode_page_heads(kv->dtype, kv->num_kv_heads, D);
+    const int64_t page_slots = (int64_t)device_cus() * vcpp::decode_page_wg_per_cu(kv->dtype, kv->num_kv_heads, D);
+    const int64_t page_ranges = page_hw > 0 ? std::max<int64_t>(1, page_slots / (kv->num_kv_heads / page_hw)) : 1;
+    int64_t G = pl.page_mode ? page_ranges : slots / groups;
     const int64_t tiles_upper = (int64_t)num_seqs * ((max_context_len + 15) / 16);
     if (partition_size > 0) {
         G = (tiles_upper * 16 + partition_size - 1) / partition_size;
@@ -159,9 +164,7 @@ DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_he
     // Page mode: the balanced split has one resident workgroup per range;
     // fixed partitions (more ranges than fit at once) are walked by that many
     // workgroups, each taking a contiguous run of ranges.
-    pl.page_grid = pl.page_mode ? (int32_t)std::min<int64_t>(
-                                      G, (int64_t)device_cus() * vcpp::decode_page_wg_per_cu(kv->dtype))
-                                : pl.num_wg;
+    pl.page_grid = pl.page_mode ? (int32_t)std::min<int64_t>(G, page_ranges) : pl.num_wg;
     pl.off_o = 0;
     const size_t blocks = (size_t)G * 2 * pairs;  // [range][slot][kv-head slot]
     pl.off_ml = pl.off_o + align256(blocks * 8 * D * sizeof(float));

@@ -64,9 +64,12 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);
 // Workgroups along y of the fp16/int8 grid (kv-head groups of up to 4 waves).
 int decode_group_count(int pairs);
 bool decode_head_dim_supported(int kv_dtype, int head_dim);
+// kv heads per workgroup of the page-staged kernel for a shape (0: the
+// shape runs the register-path kernel).
+int decode_page_heads(int kv_dtype, int num_kv_heads, int head_dim);
+// Workgroups of the page-staged kernel resident per CU for a shape.
+int decode_page_wg_per_cu(int kv_dtype, int num_kv_heads, int head_dim);
 // Shapes the page-staged kernel (decode_page_kernel) handles.
-// Workgroups of the page-staged kernel resident per CU for a page dtype.
-int decode_page_wg_per_cu(int kv_dtype);
 
 bool decode_page_mode_supported(int kv_dtype, int num_kv_heads, int group, int head_dim,
                                 int block_size);

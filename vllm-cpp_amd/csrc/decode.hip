@@ -906,8 +906,6 @@ __global__ __launch_bounds__(256) void merge_parts_kernel(DecodeParams p) {
 // one more DMA instruction: the K scale multiplies the fp32 score, the V scale
 // fp32 P before its fp16 split.
 
-constexpr int kPageWaves = 8;      // kv heads per workgroup (Hkv)
-constexpr int kPageWindow = 512;   // tiles listed in LDS at a time
 
 struct PageEntry {
     int bid;     // physical block (-1: zeros)
@@ -919,29 +917,37 @@ struct PageEntry {
     int pad0, pad1;
 };
 
-template <int KV, int D>
+// Shape of the page-staged kernel: HW kv heads per workgroup (one wave
+// each); a tile region is the 16 tokens' slice of those heads' rows.
+//  * HW 8, D 64 / 80 (BASELINE shapes): fp16 a 3-tile ring, one workgroup per
+//    CU (2 waves per SIMD); byte pages two workgroups per CU (4 waves per
+//    SIMD), whose second workgroup hides the first one's per-tile latency
+//    (a deeper single ring does not).
+//  * HW 4 (head groups of 4 kv heads, and head_dim 128): fp16 D <= 80 two
+//    workgroups per CU with 3-tile rings; fp16 D 128 (32 KiB per tile) two
+//    workgroups per CU with 2-tile rings; byte pages D <= 80 four workgroups
+//    per CU, D 128 two.
+template <int KV, int D, int HW>
 struct PageCfg {
     static constexpr bool BYTES = KV != VCPP_KV_F16;   // int8 or FP8: one byte per value
     static constexpr bool SCALED = KV == VCPP_KV_I8;   // per-(token, head) fp16 scales
     static constexpr int ES = BYTES ? 1 : 2;
-    static constexpr int RC = kPageWaves * D * ES / 16;   // 16-byte chunks per token row
+    static constexpr int RC = HW * D * ES / 16;           // 16-byte chunks per token row slice
     static constexpr int HC = D * ES / 16;                // chunks of one head in a row
-    static constexpr int SWZ = RC % 16 == 0 ? 16 : 8;     // swizzle group (chunks)
+    static constexpr int SWZ = RC % 16 == 0 ? 16 : RC % 8 == 0 ? 8 : 4;  // swizzle group (chunks)
     static constexpr int REG = 16 * RC * 16;              // bytes of one region (K or V) of a tile
     static constexpr int NI = REG / 1024;                 // DMA instructions per region
     static constexpr int NREAL = 2 * NI + (SCALED ? 1 : 0);  // + the scale instruction
-    static constexpr int PERW = (NREAL + kPageWaves - 1) / kPageWaves;
+    static constexpr int PERW = (NREAL + HW - 1) / HW;
     static constexpr int STAGE = 2 * REG + (SCALED ? 1024 : 0);
-    // Byte pages run two workgroups per CU (4 waves per SIMD, a 3-tile ring
-    // each): the second workgroup's waves hide the per-tile latency of the
-    // first, which a deeper single ring does not.  fp16 tiles are twice the
-    // bytes and need the whole LDS for 3 tiles.
-    static constexpr int WPC = BYTES ? 2 : 1;   // workgroups per CU
-    static constexpr int WPE = 2 * WPC;         // waves per SIMD
-    static constexpr int STAGES = 3;
+    static constexpr bool BIG = !BYTES && HW == 4 && D > 80;   // fp16 head_dim 128
+    static constexpr int WPC = HW == 8 ? (BYTES ? 2 : 1) : (BYTES && D <= 80 ? 4 : 2);  // workgroups per CU
+    static constexpr int WPE = WPC * HW / 4;              // waves per SIMD
+    static constexpr int STAGES = BIG ? 2 : 3;
+    static constexpr int WINDOW = WPC == 4 ? 128 : (BIG ? 256 : 512);  // tiles listed at a time
     static constexpr int OFF_JUNK = STAGES * STAGE;       // target of padding DMAs
-    static constexpr int OFF_LIST = OFF_JUNK + (PERW * kPageWaves > NREAL ? 1024 : 0);
-    static constexpr int LDS = OFF_LIST + kPageWindow * (int)sizeof(PageEntry);
+    static constexpr int OFF_LIST = OFF_JUNK + (PERW * HW > NREAL ? 1024 : 0);
+    static constexpr int LDS = OFF_LIST + WINDOW * (int)sizeof(PageEntry);
     static_assert(RC % SWZ == 0 && REG % 1024 == 0 && (D * ES) % 16 == 0, "tile shape");
     static_assert(LDS * WPC <= 160 * 1024, "LDS budget");
 };
@@ -967,13 +973,13 @@ __device__ __forceinline__ int page_slot(int gc, int rc) {
     return (gc & ~(SWZ - 1)) | ((gc & (SWZ - 1)) ^ ((gc / rc) & (SWZ - 1)));
 }
 
-template <int KV, int D>
-__global__ __launch_bounds__(kPageWaves * 64) __attribute__((amdgpu_waves_per_eu(PageCfg<KV, D>::WPE, PageCfg<KV, D>::WPE)))
+template <int KV, int D, int HW>
+__global__ __launch_bounds__(HW * 64) __attribute__((amdgpu_waves_per_eu(PageCfg<KV, D, HW>::WPE, PageCfg<KV, D, HW>::WPE)))
 void decode_page_kernel(DecodeParams p) {
-    using C = PageCfg<KV, D>;
+    using C = PageCfg<KV, D, HW>;
     constexpr bool BYTES = C::BYTES, SCALED = C::SCALED;
     constexpr int NC32 = Dims<D>::NC32, NT = Dims<D>::NT;
-    constexpr int HKV = kPageWaves;
+    constexpr int kPageWindow = C::WINDOW;
     constexpr int RC = C::RC, HC = C::HC, SWZ = C::SWZ, REG = C::REG, NI = C::NI;
     constexpr int PERW = C::PERW, STAGE = C::STAGE, STAGES = C::STAGES;
     extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -991,7 +997,11 @@ void decode_page_kernel(DecodeParams p) {
     // by the workgroup (span_of in the merge kernel).
     const int G = p.num_wg, WG = gridDim.x;
     const int r_lo = range_start(blockIdx.x, G, WG), r_hi = range_start(blockIdx.x + 1, G, WG);
-    const int kvh = wave, pair = wave;  // group <= 8: one query chunk per kv head
+    // This workgroup's kv heads: hb .. hb + HW - 1, one per wave (global
+    // head kvh; local slot `wave` in the LDS tile).  group <= 8: one query
+    // chunk per kv head.
+    const int hb = blockIdx.y * HW;
+    const int kvh = hb + wave, pair = kvh;
     const int head_base = kvh * p.group;
     const int gc = p.group;
 
@@ -1045,8 +1055,9 @@ void decode_page_kernel(DecodeParams p) {
             while (todo) {
                 const int j = __builtin_ctzll(todo);
                 todo &= todo - 1;
-                float* orow = p.out + (int64_t)(base + j) * p.num_heads * D;
-                for (int e = lane; e < p.num_heads * D; e += 64) orow[e] = 0.f;
+                // this workgroup's heads only
+                float* orow = p.out + ((int64_t)(base + j) * p.num_heads + hb * p.group) * D;
+                for (int e = lane; e < HW * p.group * D; e += 64) orow[e] = 0.f;
             }
         }
     }
@@ -1063,10 +1074,15 @@ void decode_page_kernel(DecodeParams p) {
             tok = e.tok;
 #ifdef VCPP_GATHER_DUMP
             const int gpos = e.tis * kTile + lane;
-            if (wave == 0 && lane < kTile && bid >= 0 && gpos < e.end) gather_record(p, e.seq, gpos, bid, tok + lane);
+            if (blockIdx.y == 0 && wave == 0 && lane < kTile && bid >= 0 && gpos < e.end)
+                gather_record(p, e.seq, gpos, bid, tok + lane);
 #endif
         }
-        const int64_t elem = (int64_t)(bid >= 0 ? bid : 0) * p.block_stride + (int64_t)tok * HKV * D;
+        // The workgroup's slice of each token row: rows are num_kv_heads * D
+        // elements apart and the slice starts hb * D into one (the whole row
+        // when HW == num_kv_heads, one contiguous run for the tile).
+        const int64_t row = (int64_t)p.num_kv_heads * D;
+        const int64_t elem = (int64_t)(bid >= 0 ? bid : 0) * p.block_stride + (int64_t)tok * row + (int64_t)hb * D;
 #pragma unroll
         for (int i = 0; i < PERW; ++i) {
             const int j = wave * PERW + i;  // uniform
@@ -1075,15 +1091,18 @@ void decode_page_kernel(DecodeParams p) {
                 const int pos = (j - which * NI) * 64 + lane;  // slot in the region
                 const int grp = pos & ~(SWZ - 1);
                 const int gcn = grp | ((pos & (SWZ - 1)) ^ ((grp / RC) & (SWZ - 1)));  // source chunk
+                const int gtok = gcn / RC, gch = gcn - gtok * RC;           // its token, chunk in the slice
                 const char* base = static_cast<const char*>(which ? p.v : p.k);
-                const void* src = bid >= 0 ? (const void*)(base + elem * C::ES + (int64_t)gcn * 16)
+                const void* src = bid >= 0 ? (const void*)(base + (elem + gtok * row) * C::ES + (int64_t)gch * 16)
                                            : (const void*)kZeroChunk16;
                 dma16_page(src, __builtin_amdgcn_readfirstlane(sbase + which * REG + (j - which * NI) * 1024));
             } else if (SCALED && j == 2 * NI) {
-                // lanes 0..15: K scales of head lane/2 (32 B = 2 chunks), 16..31: V scales
-                const int head = (lane >> 1) & 7, half = lane & 1;
-                const uint16_t* sp = lane >= 16 ? p.v_scale : p.k_scale;
-                const void* src = bid >= 0 && lane < 32
+                // lanes 0 .. 2 HW - 1: K scales of local head lane / 2 (32 B =
+                // 2 chunks), lanes 2 HW .. 4 HW - 1: V scales likewise
+                const bool vsc = lane >= 2 * HW;
+                const int head = hb + ((vsc ? lane - 2 * HW : lane) >> 1), half = lane & 1;
+                const uint16_t* sp = vsc ? p.v_scale : p.k_scale;
+                const void* src = bid >= 0 && lane < 4 * HW
                     ? (const void*)(sp + (int64_t)bid * p.scale_block_stride + head * p.block_size + tok + 8 * half)
                     : (const void*)kZeroChunk16;
                 dma16_page(src, __builtin_amdgcn_readfirstlane(sbase + 2 * REG));
@@ -1226,12 +1245,12 @@ void decode_page_kernel(DecodeParams p) {
 
     // LDS byte offset of chunk `chunk` of this lane's token row c, head kvh
     // (the same in the K and V regions).
-    auto kofs = [&](int chunk) { return page_slot<SWZ>(c * RC + kvh * HC + chunk, RC) * 16; };
+    auto kofs = [&](int chunk) { return page_slot<SWZ>(c * RC + wave * HC + chunk, RC) * 16; };
     // fp16: transposing V reads (tokens 4g + c/4 [+ 0..3], dims 16t + 4(c&3)).
     auto vofs = [&](int t) {
         const int tok = 4 * g + (c >> 2);
         const int dim = 16 * t + 4 * (c & 3);
-        return REG + page_slot<SWZ>(tok * RC + kvh * HC + dim / 8, RC) * 16 + (dim & 7) * 2;
+        return REG + page_slot<SWZ>(tok * RC + wave * HC + dim / 8, RC) * 16 + (dim & 7) * 2;
     };
     typedef __attribute__((address_space(3))) uint32_t lds_u32;
     typedef __attribute__((address_space(3))) i2 lds_i2;
@@ -1245,8 +1264,8 @@ void decode_page_kernel(DecodeParams p) {
         if constexpr (BYTES) {
             if constexpr (SCALED) {
                 // K scales of tokens 4g..4g+3 (head kvh), V scales likewise
-                ksw = *reinterpret_cast<lds_i2*>(sb + 2 * REG + kvh * 32 + 8 * g);
-                vsw = *reinterpret_cast<lds_i2*>(sb + 2 * REG + 256 + kvh * 32 + 8 * g);
+                ksw = *reinterpret_cast<lds_i2*>(sb + 2 * REG + wave * 32 + 8 * g);
+                vsw = *reinterpret_cast<lds_i2*>(sb + 2 * REG + 32 * HW + wave * 32 + 8 * g);
             }
 #pragma unroll
             for (int cc = 0; cc < NC32; ++cc) {
@@ -1325,7 +1344,7 @@ void decode_page_kernel(DecodeParams p) {
             for (int t = 0; t < NT; t += 2) {
                 const int j = c >> 1;
                 const int u = (j < 4 || t + 1 == NT) ? t : t + 1;
-                const int ofs = REG + page_slot<SWZ>((4 * g + (j & 3)) * RC + kvh * HC + u, RC) * 16 + 8 * (c & 1);
+                const int ofs = REG + page_slot<SWZ>((4 * g + (j & 3)) * RC + wave * HC + u, RC) * 16 + 8 * (c & 1);
                 const i2 x = __builtin_amdgcn_ds_read_tr8_b64_v2i32(reinterpret_cast<lds_i2*>(sb + ofs));
                 o[t] = mfma16(pa, bytes4_to_h4<KV>((uint32_t)x.x), o[t]);
                 if (t + 1 < NT) o[t + 1] = mfma16(pa, bytes4_to_h4<KV>((uint32_t)x.y), o[t + 1]);
@@ -1374,7 +1393,7 @@ void decode_page_kernel(DecodeParams p) {
                             load_q(s, qpre2);
                         }
                     }
-                    for (int tt = t0 + tid; tt < t1; tt += kPageWaves * 64) {
+                    for (int tt = t0 + tid; tt < t1; tt += HW * 64) {
                         const int tis = tt - S;
                         const int pos = tis * kTile;
                         const int lb = pos / p.block_size;
@@ -1418,21 +1437,34 @@ void decode_page_kernel(DecodeParams p) {
     if (cur >= 0) finalize();
 }
 
-template <int KV, int D>
+template <int KV, int D, int HW>
 hipError_t launch_page(const DecodeParams& p, hipStream_t stream) {
-    const size_t lds = PageCfg<KV, D>::LDS;
+    const size_t lds = PageCfg<KV, D, HW>::LDS;
     // The LDS limit is a per-device property of the kernel: set it once on
     // each device the library launches on (idempotent if two threads race).
     static bool attr_set[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || !attr_set[dev]) {
-        const hipError_t e = hipFuncSetAttribute((const void*)decode_page_kernel<KV, D>,
+        const hipError_t e = hipFuncSetAttribute((const void*)decode_page_kernel<KV, D, HW>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         if (dev >= 0 && dev < 64) attr_set[dev] = true;
     }
-    hipLaunchKernelGGL((decode_page_kernel<KV, D>), dim3(p.page_grid), dim3(kPageWaves * 64), lds, stream, p);
+    hipLaunchKernelGGL((decode_page_kernel<KV, D, HW>), dim3(p.page_grid, p.num_kv_heads / HW), dim3(HW * 64),
+                       lds, stream, p);
     return hipGetLastError();
+}
+
+template <int KV>
+hipError_t launch_page_kv(const DecodeParams& p, hipStream_t stream) {
+    switch (decode_page_heads(p.kv_dtype, p.num_kv_heads, p.head_dim)) {
+        case 8: return p.head_dim == 64 ? launch_page<KV, 64, 8>(p, stream) : launch_page<KV, 80, 8>(p, stream);
+        case 4:
+            if (p.head_dim == 64) return launch_page<KV, 64, 4>(p, stream);
+            if (p.head_dim == 80) return launch_page<KV, 80, 4>(p, stream);
+            return launch_page<KV, 128, 4>(p, stream);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 template <int KV, int D, int TPS, int NBUF>
@@ -1510,15 +1542,9 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
         default: return hipErrorInvalidValue;                             \
     }
     if (p.page_mode) {
-        if (p.kv_dtype == VCPP_KV_I8)
-            err = p.head_dim == 64 ? launch_page<VCPP_KV_I8, 64>(p, stream)
-                                   : launch_page<VCPP_KV_I8, 80>(p, stream);
-        else if (p.kv_dtype == VCPP_KV_FP8)
-            err = p.head_dim == 64 ? launch_page<VCPP_KV_FP8, 64>(p, stream)
-                                   : launch_page<VCPP_KV_FP8, 80>(p, stream);
-        else
-            err = p.head_dim == 64 ? launch_page<VCPP_KV_F16, 64>(p, stream)
-                                   : launch_page<VCPP_KV_F16, 80>(p, stream);
+        if (p.kv_dtype == VCPP_KV_I8) err = launch_page_kv<VCPP_KV_I8>(p, stream);
+        else if (p.kv_dtype == VCPP_KV_FP8) err = launch_page_kv<VCPP_KV_FP8>(p, stream);
+        else err = launch_page_kv<VCPP_KV_F16>(p, stream);
     } else if (p.kv_dtype == VCPP_KV_F16) {
         VCPP_DISPATCH_D(VCPP_KV_F16)
     } else if (p.kv_dtype == VCPP_KV_FP8) {
@@ -1541,16 +1567,30 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
     return err;
 }
 
-int decode_page_wg_per_cu(int kv_dtype) {
-    return kv_dtype == VCPP_KV_I8 || kv_dtype == VCPP_KV_FP8 ? 2 : 1;
+int decode_page_heads(int kv_dtype, int num_kv_heads, int head_dim) {
+    if (kv_dtype != VCPP_KV_F16 && kv_dtype != VCPP_KV_I8 && kv_dtype != VCPP_KV_FP8) return 0;
+    if ((head_dim == 64 || head_dim == 80) && num_kv_heads % 8 == 0) return 8;
+    if ((head_dim == 64 || head_dim == 80 || head_dim == 128) && num_kv_heads % 4 == 0) return 4;
+    return 0;
+}
+
+int decode_page_wg_per_cu(int kv_dtype, int num_kv_heads, int head_dim) {
+    const int hw = decode_page_heads(kv_dtype, num_kv_heads, head_dim);
+#define VCPP_WPC(KVT)                                                                  \
+    (hw == 8 ? (head_dim == 64 ? PageCfg<KVT, 64, 8>::WPC : PageCfg<KVT, 80, 8>::WPC) \
+     : head_dim == 64 ? PageCfg<KVT, 64, 4>::WPC                                       \
+     : head_dim == 80 ? PageCfg<KVT, 80, 4>::WPC : PageCfg<KVT, 128, 4>::WPC)
+    if (hw == 0) return 1;
+    if (kv_dtype == VCPP_KV_I8) return VCPP_WPC(VCPP_KV_I8);
+    if (kv_dtype == VCPP_KV_FP8) return VCPP_WPC(VCPP_KV_FP8);
+    return VCPP_WPC(VCPP_KV_F16);
+#undef VCPP_WPC
 }
 
 bool decode_page_mode_supported(int kv_dtype, int num_kv_heads, int group, int head_dim,
                                 int block_size) {
-    return (kv_dtype == VCPP_KV_F16 || kv_dtype == VCPP_KV_I8 || kv_dtype == VCPP_KV_FP8) &&
-           num_kv_heads == kPageWaves &&
-           group <= 8 &&
-           (head_dim == 64 || head_dim == 80) && block_size % kTile == 0;
+    return decode_page_heads(kv_dtype, num_kv_heads, head_dim) > 0 && group <= 8 &&
+           block_size % kTile == 0;
 }
 
 bool decode_head_dim_supported(int kv_dtype, int head_dim) {
