@@ -293,32 +293,53 @@ def bench_config5(torch, pyvcpp, args):
     prefix = torch.full((4,), 1024, dtype=torch.int32, device=dev)
     dctx_d = dctx.to(dev)
     need = pyvcpp.decode_workspace_size(pages, 128, H, 8192, 0)
+
+    need = max(need, pyvcpp.mixed_workspace_size(pages, 128, H, 8192, ptab.shape[1]))
     ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=dev)
 
-    def step():
+    def two_launches():
         pyvcpp.paged_decode(pages, qd, od, dtab, dctx_d, 8192, H, workspace=ws)
         pyvcpp.paged_prefill(pages, qp.view(torch.int16), op, ptab, q_start, prefix, 512, H)
-    dt = timed(torch, step, args.config_steps)
-    pyvcpp.profile_enable(True)
-    for _ in range(args.config_steps):
-        step()
-    torch.cuda.synchronize()
-    times = {name: pyvcpp.profile_read(kid) for name, kid in
-             (("decode", pyvcpp.KERNEL_DECODE), ("merge", pyvcpp.KERNEL_MERGE),
-              ("prefill", pyvcpp.KERNEL_PREFILL))}
-    pyvcpp.profile_enable(False)
+
+    def mixed_step():
+        pyvcpp.paged_mixed_step(pages, qd, od, dtab, dctx_d, 8192, qp.view(torch.int16), op, ptab,
+                                q_start, prefix, 512, H, workspace=ws)
+
+    def fused_one_launch():  # the opt-in single-launch form of the same call
+        os.environ["VCPP_MIXED_FUSED"] = "1"
+        try:
+            mixed_step()
+        finally:
+            del os.environ["VCPP_MIXED_FUSED"]
+
     dbytes = (int(dctx.sum()) * (2 * HKV * D + 2 * HKV * 2) + 128 * H * D * 8
               + sum(nblk[:128]) * 4)
     pairs = 4 * sum(1024 + i + 1 for i in range(512))
     flops = 4 * D * H * pairs
     t_star = max(dbytes / (HBM_PEAK_TBS * 1e12), flops / (F16_MFMA_PEAK_TFS * 1e12))
-    us = {k: round(v[0] / max(v[1], 1) * 1e3, 1) for k, v in times.items()}
-    return {"metric": "int8 mixed step: fraction of T* = max(bytes/8 TB/s, flops/2.5 PF)",
+    variants = {}
+    for name, step in (("two_launches", two_launches), ("mixed_step", mixed_step),
+                       ("fused_one_launch", fused_one_launch)):
+        dt = timed(torch, step, args.config_steps)
+        pyvcpp.profile_enable(True)
+        for _ in range(args.config_steps):
+            step()
+        torch.cuda.synchronize()
+        times = {k: pyvcpp.profile_read(kid) for k, kid in
+                 (("decode", pyvcpp.KERNEL_DECODE), ("merge", pyvcpp.KERNEL_MERGE),
+                  ("prefill", pyvcpp.KERNEL_PREFILL), ("mixed", pyvcpp.KERNEL_MIXED))}
+        pyvcpp.profile_enable(False)
+        us = {k: round(v[0] / max(v[1], 1) * 1e3, 1) for k, v in times.items() if v[1] > 0}
+        variants[name] = {"ms_per_step": round(dt * 1e3, 4), "fraction_of_t_star": round(t_star / dt, 4),
+                          "kernel_us": us}
+        if name == "two_launches":
+            variants[name]["decode_TB/s_in_kernel"] = round(dbytes / (us["decode"] * 1e-6) / 1e12, 3)
+            variants[name]["prefill_TFLOP/s_in_kernel"] = round(flops / (us["prefill"] * 1e-6) / 1e12, 1)
+    dt = variants["mixed_step"]["ms_per_step"] * 1e-3
+    return {"metric": "int8 mixed step (vcpp_paged_mixed_step): fraction of T* = max(bytes/8 TB/s, flops/2.5 PF)",
             "value": round(t_star / dt, 4), "unit": "fraction",
             "ms_per_step": round(dt * 1e3, 4), "t_star_ms": round(t_star * 1e3, 4),
-            "decode_TB/s_in_kernel": round(dbytes / (us["decode"] * 1e-6) / 1e12, 3),
-            "prefill_TFLOP/s_in_kernel": round(flops / (us["prefill"] * 1e-6) / 1e12, 1),
-            "kernel_us": us, "steps": args.config_steps,
+            "variants": variants, "steps": args.config_steps,
             "config": {"workload": "BASELINE config 5: 128 decode seqs ctx U[1024,8192] + 4 prefill "
                                    "chunks x 512 on 1024-token prefixes, int8 KV + fp16 scales, GQA 8:1, "
                                    "head_dim 80", "decode_bytes": dbytes, "prefill_flops": flops}}

@@ -180,6 +180,37 @@ int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
                        const int32_t* q_start, const int32_t* prefix_lens, int32_t num_chunks,
                        int32_t max_chunk_len, int32_t num_heads, void* stream);
 
+/* ---- v2: one scheduler step with decodes and prefill chunks ------------- */
+
+/*
+ * A step whose ScheduleOutput (src/scheduler.h:14-23) holds both decoding
+ * requests and prefill chunks, served together as the engine's step does
+ * (src/paged_engine.cpp:254-269): the decode of vcpp_paged_decode (arguments
+ * d_* / dq / dout / num_seqs / max_context_len, balanced split) and the
+ * prefill of vcpp_paged_prefill (pq / pout / p_* / q_start / prefix_lens /
+ * num_chunks / max_chunk_len) over the same pages, with the same results.
+ * Where the shape allows (fp16, int8 or FP8 pages; head_dim 64 or 80;
+ * num_kv_heads a multiple of 4; <= 8 query heads per kv head; a CU count that
+ * is a multiple of 8) both run in ONE launch that keeps the HBM-bound decode
+ * and the MFMA-bound prefill on every CU at once, followed by the decode's
+ * merge; otherwise as the two calls on `stream`, decode first.  Either side
+ * may be empty (num_seqs == 0, or num_chunks == 0).
+ *   workspace    device scratch of at least vcpp_mixed_workspace_size(...)
+ */
+int vcpp_paged_mixed_step(const vcpp_kv_pages* kv, const float* dq, float* dout,
+                          const int32_t* d_block_tables, int32_t d_max_blocks_per_seq,
+                          const int32_t* d_table_lens, const int32_t* d_context_lens, int32_t num_seqs,
+                          int32_t max_context_len, const uint16_t* pq, float* pout,
+                          const int32_t* p_block_tables, int32_t p_max_blocks_per_seq,
+                          const int32_t* q_start, const int32_t* prefix_lens, int32_t num_chunks,
+                          int32_t max_chunk_len, int32_t num_heads, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* Workspace bytes vcpp_paged_mixed_step needs on the current device
+ * (max_blocks_per_chunk = its p_max_blocks_per_seq). */
+size_t vcpp_mixed_workspace_size(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_heads,
+                                 int32_t max_context_len, int32_t max_blocks_per_chunk);
+
 /* ---- v2: writing K/V into the pages ------------------------------------ */
 
 /*
@@ -307,6 +338,7 @@ void head_norm_cuda(float* x, const float* weight, float eps, int32_t num_heads,
 #define VCPP_KERNEL_DECODE 0  /* decode attention (fp16/int8/fp8 MFMA or fp32) */
 #define VCPP_KERNEL_MERGE 1   /* split-K log-sum-exp merge */
 #define VCPP_KERNEL_PREFILL 2 /* chunked causal prefill */
+#define VCPP_KERNEL_MIXED 3   /* fused decode + prefill step (vcpp_paged_mixed_step) */
 
 /* Start (on != 0) or stop per-kernel timing and clear the counters.  While on,
  * each launch records a HIP event before and after the kernel on the stream

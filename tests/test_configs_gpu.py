@@ -57,10 +57,11 @@ def test_config4_long_context(cuda, config4, partition):
     assert_close(got, want, *TOL, what="config4 P=%d" % partition)
 
 
-def test_config5_int8_mixed_step(cuda):
+@pytest.fixture(scope="module")
+def config5():
     """128 decode sequences (ctx U[1024, 8192]) plus 4 prefill chunks of 512
-    tokens on 1024-token prefixes, int8 pages with fp16 scales, run as one
-    step (decode launch, then prefill launch, same stream)."""
+    tokens on 1024-token prefixes, int8 pages with fp16 scales; oracle outputs
+    of every decode and of sampled prefill rows."""
     dctx = O.uniform_int(501, 128, 1024, 8192)
     plen = np.full(4, 1024 + 512, np.int32)
     nb = int(np.ceil(1.25 * (dctx.sum() + plen.sum()) / 16))
@@ -71,21 +72,34 @@ def test_config5_int8_mixed_step(cuda):
     q_start = np.arange(0, 4 * 512 + 1, 512, dtype=np.int32)
     prefix = np.full(4, 1024, np.int32)
     qp = O.normal(505, (4 * 512, 64, 80)).astype(np.float16)
-
-    dp = DevPool(pool)
-    qdd = dev(qd)
-    out_d = torch.full_like(qdd, float("nan"))
-    out_p = torch.full(qp.shape, float("nan"), dtype=torch.float32, device="cuda:0")
-    pyvcpp.paged_decode(dp.pages, qdd, out_d, dev(dtab), dev(dctx), int(dctx.max()), 64)
-    pyvcpp.paged_prefill(dp.pages, dev(qp.view(np.uint16)), out_p, dev(ptab), dev(q_start),
-                         dev(prefix), 512, 64)
-    torch.cuda.synchronize()
-
     ref = fp32_view(pool)
     want_d = O.decode(ref, qd, dtab, dctx, 64, nthreads=NTHREADS)
-    assert_close(out_d.cpu().numpy(), want_d, *TOL, what="config5 decode")
     rng = np.random.default_rng(5)
     rows = np.unique(np.concatenate([rng.integers(0, 2048, 96), q_start[:-1], q_start[1:] - 1]))
     want_p = oracle_prefill_rows(ref, qp.astype(np.float32), ptab, q_start, prefix, 64, rows,
                                  nthreads=NTHREADS)
-    assert_close(out_p.cpu().numpy()[rows], want_p, *TOL, what="config5 prefill rows")
+    return dict(pool=pool, dctx=dctx, dtab=dtab, ptab=ptab, qd=qd, q_start=q_start, prefix=prefix,
+                qp=qp, want_d=want_d, rows=rows, want_p=want_p)
+
+
+@pytest.mark.parametrize("mode", ["two_launches", "mixed_step", "mixed_step_fused"])
+def test_config5_int8_mixed_step(cuda, config5, mode, monkeypatch):
+    """BASELINE config 5 as one step: decode then prefill on one stream, or
+    vcpp_paged_mixed_step (two launches, or with VCPP_MIXED_FUSED=1 one fused
+    launch + the decode merge)."""
+    monkeypatch.setenv("VCPP_MIXED_FUSED", "1" if mode == "mixed_step_fused" else "0")
+    c = config5
+    dp = DevPool(c["pool"])
+    qdd = dev(c["qd"])
+    out_d = torch.full_like(qdd, float("nan"))
+    out_p = torch.full(c["qp"].shape, float("nan"), dtype=torch.float32, device="cuda:0")
+    args_p = (dev(c["qp"].view(np.uint16)), out_p, dev(c["ptab"]), dev(c["q_start"]), dev(c["prefix"]), 512)
+    if mode == "two_launches":
+        pyvcpp.paged_decode(dp.pages, qdd, out_d, dev(c["dtab"]), dev(c["dctx"]), int(c["dctx"].max()), 64)
+        pyvcpp.paged_prefill(dp.pages, *args_p, 64)
+    else:
+        pyvcpp.paged_mixed_step(dp.pages, qdd, out_d, dev(c["dtab"]), dev(c["dctx"]), int(c["dctx"].max()),
+                                *args_p, 64)
+    torch.cuda.synchronize()
+    assert_close(out_d.cpu().numpy(), c["want_d"], *TOL, what="config5 decode (%s)" % mode)
+    assert_close(out_p.cpu().numpy()[c["rows"]], c["want_p"], *TOL, what="config5 prefill rows (%s)" % mode)

@@ -101,8 +101,10 @@ struct DecodePlan {
     size_t off_o = 0, off_ml = 0, bytes = 0;
 };
 
+// fused_grid > 0: the decode side of the fused mixed step, whose decode
+// workers (fused_grid per kv-head group of 4) walk the balanced split.
 DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_heads,
-                       int32_t max_context_len, int32_t partition_size) {
+                       int32_t max_context_len, int32_t partition_size, int32_t fused_grid = 0) {
     DecodePlan pl;
     const int D = kv->head_dim;
     if (kv->dtype == VCPP_KV_F32) {
@@ -153,6 +155,10 @@ DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_he
     const int64_t page_slots = (int64_t)device_cus() * vcpp::decode_page_wg_per_cu(kv->dtype, kv->num_kv_heads, D);
     const int64_t page_ranges = page_hw > 0 ? std::max<int64_t>(1, page_slots / (kv->num_kv_heads / page_hw)) : 1;
     int64_t G = pl.page_mode ? page_ranges : slots / groups;
+    if (fused_grid > 0) {
+        pl.page_mode = true;
+        G = fused_grid;
+    }
     const int64_t tiles_upper = (int64_t)num_seqs * ((max_context_len + 15) / 16);
     if (partition_size > 0) {
         G = (tiles_upper * 16 + partition_size - 1) / partition_size;
@@ -164,7 +170,8 @@ DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_he
     // Page mode: the balanced split has one resident workgroup per range;
     // fixed partitions (more ranges than fit at once) are walked by that many
     // workgroups, each taking a contiguous run of ranges.
-    pl.page_grid = pl.page_mode ? (int32_t)std::min<int64_t>(G, page_ranges) : pl.num_wg;
+    pl.page_grid = pl.page_mode ? (int32_t)std::min<int64_t>(G, fused_grid > 0 ? fused_grid : page_ranges)
+                                : pl.num_wg;
     pl.off_o = 0;
     const size_t blocks = (size_t)G * 2 * pairs;  // [range][slot][kv-head slot]
     pl.off_ml = pl.off_o + align256(blocks * 8 * D * sizeof(float));
@@ -329,12 +336,14 @@ size_t vcpp_decode_workspace_size(const vcpp_kv_pages* kv, int32_t num_seqs, int
     return plan_decode(kv, num_seqs, num_heads, max_context_len, partition_size).bytes;
 }
 
-int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
-                      const int32_t* block_tables, int32_t max_blocks_per_seq,
-                      const int32_t* table_lens, const int32_t* context_lens, int32_t num_seqs,
-                      int32_t max_context_len, int32_t num_heads, int32_t partition_size,
-                      void* workspace, size_t workspace_bytes, void* stream) {
-    g_last_error.clear();
+}  // extern "C"
+
+namespace {
+
+// Validates a decode call's arguments (not its workspace).
+int check_decode(const vcpp_kv_pages* kv, const float* q, float* out, const int32_t* block_tables,
+                 int32_t max_blocks_per_seq, const int32_t* context_lens, int32_t num_seqs,
+                 int32_t max_context_len, int32_t num_heads, int32_t partition_size) {
     int rc = check_pages(kv);
     if (rc != VCPP_OK) return rc;
     if (num_seqs < 0) return fail(VCPP_E_INVALID, "num_seqs must be >= 0");
@@ -350,13 +359,21 @@ int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
     if (partition_size < 0 || partition_size % 16 != 0 || partition_size > kMaxPartition)
         return fail(VCPP_E_INVALID, "partition_size %d must be 0 or a multiple of 16 <= %d",
                     partition_size, kMaxPartition);
-    const DecodePlan pl = plan_decode(kv, num_seqs, num_heads, max_context_len, partition_size);
-    if (pl.max_parts > 65535) return fail(VCPP_E_UNSUPPORTED, "too many partitions (%d)", pl.max_parts);
-    const size_t need = pl.bytes;
-    if (need > 0 && (!workspace || workspace_bytes < need))
-        return fail(VCPP_E_WORKSPACE, "decode needs %zu workspace bytes, got %zu", need,
-                    workspace ? workspace_bytes : (size_t)0);
+    if (kv->dtype != VCPP_KV_F32 && (int64_t)kv->num_kv_heads * ((num_heads / kv->num_kv_heads + 7) / 8) > 65535 * 8)
+        return fail(VCPP_E_UNSUPPORTED, "too many kv heads");
+    if (kv->dtype == VCPP_KV_F32 && (int64_t)kv->num_kv_heads * ((num_heads / kv->num_kv_heads + 7) / 8) > 65535)
+        return fail(VCPP_E_UNSUPPORTED, "too many kv heads");
+    if (kv->dtype == VCPP_KV_F32 && num_seqs > 65535)
+        return fail(VCPP_E_UNSUPPORTED, "fp32 pages: too many sequences (%d)", num_seqs);
+    return VCPP_OK;
+}
 
+// The launch parameters of a checked decode call under plan pl.
+vcpp::DecodeParams decode_params(const vcpp_kv_pages* kv, const float* q, float* out,
+                                 const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                 const int32_t* table_lens, const int32_t* context_lens, int32_t num_seqs,
+                                 int32_t max_context_len, int32_t num_heads, int32_t partition_size,
+                                 const DecodePlan& pl, void* workspace) {
     vcpp::DecodeParams p{};
     p.k = kv->k;
     p.v = kv->v;
@@ -390,7 +407,7 @@ int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
     // tiles to ranges on the same axis).
     p.switch_tiles = pl.page_mode && partition_size == 0 ? kSwitchTiles : 0;
     p.ctx_cap = max_context_len;
-    if (need > 0) {
+    if (pl.bytes > 0) {
         p.ws_o = reinterpret_cast<float*>(ws + pl.off_o);
         p.ws_ml = reinterpret_cast<float2*>(ws + pl.off_ml);
     }
@@ -403,20 +420,20 @@ int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
     p.gather_dump = g_gather_dump;
     p.gather_stride = g_gather_stride;
 #endif
-    if (p.pairs > (kv->dtype == VCPP_KV_F32 ? 65535 : 65535 * 8))
-        return fail(VCPP_E_UNSUPPORTED, "too many kv heads");
-    if (kv->dtype == VCPP_KV_F32 && num_seqs > 65535)
-        return fail(VCPP_E_UNSUPPORTED, "fp32 pages: too many sequences (%d)", num_seqs);
-    hipError_t e = vcpp::launch_decode(p, static_cast<hipStream_t>(stream));
-    if (e != hipSuccess) return hip_fail(e, "decode launch");
+    return p;
+}
+
+int check_workspace(const DecodePlan& pl, void* workspace, size_t workspace_bytes) {
+    if (pl.bytes > 0 && (!workspace || workspace_bytes < pl.bytes))
+        return fail(VCPP_E_WORKSPACE, "decode needs %zu workspace bytes, got %zu", pl.bytes,
+                    workspace ? workspace_bytes : (size_t)0);
     return VCPP_OK;
 }
 
-int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
-                       const int32_t* block_tables, int32_t max_blocks_per_seq,
-                       const int32_t* q_start, const int32_t* prefix_lens, int32_t num_chunks,
-                       int32_t max_chunk_len, int32_t num_heads, void* stream) {
-    g_last_error.clear();
+// Validates a prefill call's arguments.
+int check_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out, const int32_t* block_tables,
+                  int32_t max_blocks_per_seq, const int32_t* q_start, const int32_t* prefix_lens,
+                  int32_t num_chunks, int32_t max_chunk_len, int32_t num_heads) {
     int rc = check_pages(kv);
     if (rc != VCPP_OK) return rc;
     if (kv->dtype == VCPP_KV_F32)
@@ -438,6 +455,15 @@ int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
     if (vcpp::prefill_lds_bytes(kv->dtype, kv->head_dim, max_blocks_per_seq) > 160 * 1024)
         return fail(VCPP_E_UNSUPPORTED, "prefill block table of %d entries exceeds the LDS budget",
                     max_blocks_per_seq);
+    if ((int64_t)kv->num_kv_heads * vcpp::prefill_head_groups(num_heads / kv->num_kv_heads) > 65535)
+        return fail(VCPP_E_UNSUPPORTED, "too many heads");
+    return VCPP_OK;
+}
+
+vcpp::PrefillParams prefill_params(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
+                                   const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                   const int32_t* q_start, const int32_t* prefix_lens, int32_t num_chunks,
+                                   int32_t max_chunk_len, int32_t num_heads) {
     vcpp::PrefillParams p{};
     p.k = kv->k;
     p.v = kv->v;
@@ -455,8 +481,6 @@ int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
     p.num_heads = num_heads;
     p.group = num_heads / kv->num_kv_heads;
     p.head_groups = vcpp::prefill_head_groups(p.group);
-    if ((int64_t)kv->num_kv_heads * p.head_groups > 65535)
-        return fail(VCPP_E_UNSUPPORTED, "too many heads");
     p.block_tables = block_tables;
     p.q_start = q_start;
     p.prefix_lens = prefix_lens;
@@ -469,8 +493,118 @@ int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
     p.gather_dump = g_gather_dump;
     p.gather_stride = g_gather_stride;
 #endif
+    return p;
+}
+
+// Decode workgroups per kv-head group of the fused mixed step for this call
+// (0: run decode and prefill as two launches).  The fused launch is opt-in
+// (VCPP_MIXED_FUSED=1): on BASELINE config 5 it measured 388 us against
+// 291 us for the two launches.  Its decode side needs the page-staged
+// kernel's alignment, its prefill side three workgroups' LDS per CU.
+int32_t mixed_grid(const vcpp_kv_pages* kv, int32_t num_heads, int32_t p_max_blocks) {
+    const char* e = getenv("VCPP_MIXED_FUSED");
+    if (!e || e[0] != '1') return 0;
+    if (kv->dtype == VCPP_KV_F32 || num_heads % kv->num_kv_heads != 0) return 0;
+    const bool bytes = kv->dtype == VCPP_KV_I8 || kv->dtype == VCPP_KV_FP8;
+    if (bytes && (kv->block_stride % 16 != 0 || reinterpret_cast<uintptr_t>(kv->k) % 16 != 0 ||
+                  reinterpret_cast<uintptr_t>(kv->v) % 16 != 0))
+        return 0;
+    if (kv->dtype == VCPP_KV_I8 &&
+        (kv->scale_block_stride % 8 != 0 || reinterpret_cast<uintptr_t>(kv->k_scale) % 16 != 0 ||
+         reinterpret_cast<uintptr_t>(kv->v_scale) % 16 != 0))
+        return 0;
+    if (vcpp::mixed_lds_bytes(kv->dtype, kv->head_dim, p_max_blocks) * 3 > 160 * 1024) return 0;
+    return vcpp::mixed_decode_grid(kv->dtype, kv->num_kv_heads, num_heads / kv->num_kv_heads,
+                                   kv->head_dim, kv->block_size, device_cus());
+}
+
+}  // namespace
+
+extern "C" {
+
+int vcpp_paged_decode(const vcpp_kv_pages* kv, const float* q, float* out,
+                      const int32_t* block_tables, int32_t max_blocks_per_seq,
+                      const int32_t* table_lens, const int32_t* context_lens, int32_t num_seqs,
+                      int32_t max_context_len, int32_t num_heads, int32_t partition_size,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+    g_last_error.clear();
+    int rc = check_decode(kv, q, out, block_tables, max_blocks_per_seq, context_lens, num_seqs,
+                          max_context_len, num_heads, partition_size);
+    if (rc != VCPP_OK || num_seqs == 0) return rc;
+    const DecodePlan pl = plan_decode(kv, num_seqs, num_heads, max_context_len, partition_size);
+    if (pl.max_parts > 65535) return fail(VCPP_E_UNSUPPORTED, "too many partitions (%d)", pl.max_parts);
+    rc = check_workspace(pl, workspace, workspace_bytes);
+    if (rc != VCPP_OK) return rc;
+    const vcpp::DecodeParams p = decode_params(kv, q, out, block_tables, max_blocks_per_seq, table_lens,
+                                               context_lens, num_seqs, max_context_len, num_heads,
+                                               partition_size, pl, workspace);
+    hipError_t e = vcpp::launch_decode(p, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "decode launch");
+    return VCPP_OK;
+}
+
+int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
+                       const int32_t* block_tables, int32_t max_blocks_per_seq,
+                       const int32_t* q_start, const int32_t* prefix_lens, int32_t num_chunks,
+                       int32_t max_chunk_len, int32_t num_heads, void* stream) {
+    g_last_error.clear();
+    int rc = check_prefill(kv, q, out, block_tables, max_blocks_per_seq, q_start, prefix_lens, num_chunks,
+                           max_chunk_len, num_heads);
+    if (rc != VCPP_OK || num_chunks == 0 || max_chunk_len == 0) return rc;
+    const vcpp::PrefillParams p = prefill_params(kv, q, out, block_tables, max_blocks_per_seq, q_start,
+                                                 prefix_lens, num_chunks, max_chunk_len, num_heads);
     hipError_t e = vcpp::launch_prefill(p, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "prefill launch");
+    return VCPP_OK;
+}
+
+size_t vcpp_mixed_workspace_size(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_heads,
+                                 int32_t max_context_len, int32_t max_blocks_per_chunk) {
+    if (!kv || kv->num_kv_heads <= 0 || num_heads <= 0 || num_seqs <= 0) return 0;
+    const size_t two = plan_decode(kv, num_seqs, num_heads, max_context_len, 0).bytes;
+    const int32_t fg = mixed_grid(kv, num_heads, max_blocks_per_chunk);
+    const size_t one = fg > 0 ? plan_decode(kv, num_seqs, num_heads, max_context_len, 0, fg).bytes : 0;
+    return std::max(one, two);
+}
+
+int vcpp_paged_mixed_step(const vcpp_kv_pages* kv, const float* dq, float* dout,
+                          const int32_t* d_block_tables, int32_t d_max_blocks_per_seq,
+                          const int32_t* d_table_lens, const int32_t* d_context_lens, int32_t num_seqs,
+                          int32_t max_context_len, const uint16_t* pq, float* pout,
+                          const int32_t* p_block_tables, int32_t p_max_blocks_per_seq,
+                          const int32_t* q_start, const int32_t* prefix_lens, int32_t num_chunks,
+                          int32_t max_chunk_len, int32_t num_heads, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+    g_last_error.clear();
+    int rc = check_decode(kv, dq, dout, d_block_tables, d_max_blocks_per_seq, d_context_lens, num_seqs,
+                          max_context_len, num_heads, 0);
+    if (rc != VCPP_OK) return rc;
+    rc = check_prefill(kv, pq, pout, p_block_tables, p_max_blocks_per_seq, q_start, prefix_lens, num_chunks,
+                       max_chunk_len, num_heads);
+    if (rc != VCPP_OK) return rc;
+    const bool has_p = num_chunks > 0 && max_chunk_len > 0;
+    const int32_t fg = num_seqs > 0 && has_p ? mixed_grid(kv, num_heads, p_max_blocks_per_seq) : 0;
+    if (fg == 0) {  // two launches on the stream: decode, then prefill
+        if (num_seqs > 0) {
+            rc = vcpp_paged_decode(kv, dq, dout, d_block_tables, d_max_blocks_per_seq, d_table_lens,
+                                   d_context_lens, num_seqs, max_context_len, num_heads, 0, workspace,
+                                   workspace_bytes, stream);
+            if (rc != VCPP_OK) return rc;
+        }
+        if (!has_p) return VCPP_OK;
+        return vcpp_paged_prefill(kv, pq, pout, p_block_tables, p_max_blocks_per_seq, q_start, prefix_lens,
+                                  num_chunks, max_chunk_len, num_heads, stream);
+    }
+    const DecodePlan pl = plan_decode(kv, num_seqs, num_heads, max_context_len, 0, fg);
+    rc = check_workspace(pl, workspace, workspace_bytes);
+    if (rc != VCPP_OK) return rc;
+    const vcpp::DecodeParams dp = decode_params(kv, dq, dout, d_block_tables, d_max_blocks_per_seq, d_table_lens,
+                                                d_context_lens, num_seqs, max_context_len, num_heads, 0, pl,
+                                                workspace);
+    const vcpp::PrefillParams pp = prefill_params(kv, pq, pout, p_block_tables, p_max_blocks_per_seq, q_start,
+                                                  prefix_lens, num_chunks, max_chunk_len, num_heads);
+    hipError_t e = vcpp::launch_mixed(dp, pp, device_cus(), static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "mixed step launch");
     return VCPP_OK;
 }
 

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "prefill.h"
 #include "vcpp_attention.h"
 
 namespace vcpp {
@@ -61,6 +62,17 @@ struct DecodeParams {
 };
 
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);
+
+// The fused mixed step: one launch of 3 workgroups per CU (cus a multiple of
+// 8), two prefill workers and one decode worker on each CU, then the decode
+// merge.  dp is planned for the fused split (mixed_decode_grid); pp as for
+// launch_prefill.
+hipError_t launch_mixed(const DecodeParams& dp, const PrefillParams& pp, int cus, hipStream_t stream);
+// Decode workgroups per kv-head group of the fused step (0: the shape has no
+// fused step).
+int mixed_decode_grid(int kv_dtype, int num_kv_heads, int group, int head_dim, int block_size, int cus);
+// Dynamic LDS bytes of the fused kernel (prefill tables of max_blocks entries).
+size_t mixed_lds_bytes(int kv_dtype, int head_dim, int max_blocks);
 // Workgroups along y of the fp16/int8 grid (kv-head groups of up to 4 waves).
 int decode_group_count(int pairs);
 bool decode_head_dim_supported(int kv_dtype, int head_dim);

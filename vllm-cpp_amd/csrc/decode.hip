@@ -53,6 +53,7 @@
 // fp32 pages use a plain VALU kernel over fixed partitions (parity path).
 #include "decode.h"
 #include "device_common.h"
+#include "prefill_body.h"
 #include "profile.h"
 
 #include <cstdlib>
@@ -927,7 +928,10 @@ struct PageEntry {
 //    workgroups per CU with 3-tile rings; fp16 D 128 (32 KiB per tile) two
 //    workgroups per CU with 2-tile rings; byte pages D <= 80 four workgroups
 //    per CU, D 128 two.
-template <int KV, int D, int HW>
+// F: the decode side of the fused mixed-step kernel (HW 4, three workgroups
+// per CU): byte pages a 4-tile ring, fp16 a 2-tile ring, 128 tiles listed at
+// a time, so that its LDS stays within a third of a CU.
+template <int KV, int D, int HW, bool F = false>
 struct PageCfg {
     static constexpr bool BYTES = KV != VCPP_KV_F16;   // int8 or FP8: one byte per value
     static constexpr bool SCALED = KV == VCPP_KV_I8;   // per-(token, head) fp16 scales
@@ -941,10 +945,10 @@ struct PageCfg {
     static constexpr int PERW = (NREAL + HW - 1) / HW;
     static constexpr int STAGE = 2 * REG + (SCALED ? 1024 : 0);
     static constexpr bool BIG = !BYTES && HW == 4 && D > 80;   // fp16 head_dim 128
-    static constexpr int WPC = HW == 8 ? (BYTES ? 2 : 1) : (BYTES && D <= 80 ? 4 : 2);  // workgroups per CU
+    static constexpr int WPC = F ? 3 : HW == 8 ? (BYTES ? 2 : 1) : (BYTES && D <= 80 ? 4 : 2);  // workgroups per CU
     static constexpr int WPE = WPC * HW / 4;              // waves per SIMD
-    static constexpr int STAGES = BIG ? 2 : 3;
-    static constexpr int WINDOW = WPC == 4 ? 128 : (BIG ? 256 : 512);  // tiles listed at a time
+    static constexpr int STAGES = F ? (BYTES ? 4 : 2) : BIG ? 2 : 3;
+    static constexpr int WINDOW = F || WPC == 4 ? 128 : (BIG ? 256 : 512);  // tiles listed at a time
     static constexpr int OFF_JUNK = STAGES * STAGE;       // target of padding DMAs
     static constexpr int OFF_LIST = OFF_JUNK + (PERW * HW > NREAL ? 1024 : 0);
     static constexpr int LDS = OFF_LIST + WINDOW * (int)sizeof(PageEntry);
@@ -973,10 +977,12 @@ __device__ __forceinline__ int page_slot(int gc, int rc) {
     return (gc & ~(SWZ - 1)) | ((gc & (SWZ - 1)) ^ ((gc / rc) & (SWZ - 1)));
 }
 
-template <int KV, int D, int HW>
-__global__ __launch_bounds__(HW * 64) __attribute__((amdgpu_waves_per_eu(PageCfg<KV, D, HW>::WPE, PageCfg<KV, D, HW>::WPE)))
-void decode_page_kernel(DecodeParams p) {
-    using C = PageCfg<KV, D, HW>;
+// One workgroup of the page-staged decode: it walks ranges [r_lo, r_hi) of
+// the split (bx of the nbx workgroups per kv-head group) for kv heads
+// by * HW .. + HW - 1.
+template <int KV, int D, int HW, bool F>
+__device__ __forceinline__ void decode_page_body(const DecodeParams& p, int bx, int by, int nbx) {
+    using C = PageCfg<KV, D, HW, F>;
     constexpr bool BYTES = C::BYTES, SCALED = C::SCALED;
     constexpr int NC32 = Dims<D>::NC32, NT = Dims<D>::NT;
     constexpr int kPageWindow = C::WINDOW;
@@ -995,12 +1001,12 @@ void decode_page_kernel(DecodeParams p) {
     // partitions, whose online softmax combines them in registers.  Either
     // way a workgroup leaves at most one fragment per sequence end, indexed
     // by the workgroup (span_of in the merge kernel).
-    const int G = p.num_wg, WG = gridDim.x;
-    const int r_lo = range_start(blockIdx.x, G, WG), r_hi = range_start(blockIdx.x + 1, G, WG);
+    const int G = p.num_wg, WG = nbx;
+    const int r_lo = range_start(bx, G, WG), r_hi = range_start(bx + 1, G, WG);
     // This workgroup's kv heads: hb .. hb + HW - 1, one per wave (global
     // head kvh; local slot `wave` in the LDS tile).  group <= 8: one query
     // chunk per kv head.
-    const int hb = blockIdx.y * HW;
+    const int hb = by * HW;
     const int kvh = hb + wave, pair = kvh;
     const int head_base = kvh * p.group;
     const int gc = p.group;
@@ -1039,7 +1045,7 @@ void decode_page_kernel(DecodeParams p) {
         return T;
     };
     const int a = real_of(range_start(r_lo, Tv, G)), b = real_of(range_start(r_hi, Tv, G));
-    const bool zero_owner_tail = (T == 0 && blockIdx.x == 0) || (T > 0 && (int)blockIdx.x == WG - 1);
+    const bool zero_owner_tail = (T == 0 && bx == 0) || (T > 0 && bx == WG - 1);
 
     // Zero the outputs of empty sequences this range owns (wave 0).
     if (wave == 0) {
@@ -1074,7 +1080,7 @@ void decode_page_kernel(DecodeParams p) {
             tok = e.tok;
 #ifdef VCPP_GATHER_DUMP
             const int gpos = e.tis * kTile + lane;
-            if (blockIdx.y == 0 && wave == 0 && lane < kTile && bid >= 0 && gpos < e.end)
+            if (by == 0 && wave == 0 && lane < kTile && bid >= 0 && gpos < e.end)
                 gather_record(p, e.seq, gpos, bid, tok + lane);
 #endif
         }
@@ -1145,7 +1151,7 @@ void decode_page_kernel(DecodeParams p) {
         const bool odd = (c & 1) != 0;
         const int rr = odd ? rk1 : rk0;
         const int h = 4 * (g & 1) + rr;
-        const int64_t blk = ((int64_t)blockIdx.x * 2 + slot) * p.pairs + pair;
+        const int64_t blk = ((int64_t)bx * 2 + slot) * p.pairs + pair;
         float* orow = complete ? p.out + ((int64_t)cur * p.num_heads + head_base + h) * D
                                : p.ws_o + (blk * 8 + h) * D;
         float lsel = lh[0];
@@ -1438,6 +1444,12 @@ void decode_page_kernel(DecodeParams p) {
 }
 
 template <int KV, int D, int HW>
+__global__ __launch_bounds__(HW * 64) __attribute__((amdgpu_waves_per_eu(PageCfg<KV, D, HW>::WPE, PageCfg<KV, D, HW>::WPE)))
+void decode_page_kernel(DecodeParams p) {
+    decode_page_body<KV, D, HW, false>(p, blockIdx.x, blockIdx.y, gridDim.x);
+}
+
+template <int KV, int D, int HW>
 hipError_t launch_page(const DecodeParams& p, hipStream_t stream) {
     const size_t lds = PageCfg<KV, D, HW>::LDS;
     // The LDS limit is a per-device property of the kernel: set it once on
@@ -1452,6 +1464,87 @@ hipError_t launch_page(const DecodeParams& p, hipStream_t stream) {
     }
     hipLaunchKernelGGL((decode_page_kernel<KV, D, HW>), dim3(p.page_grid, p.num_kv_heads / HW), dim3(HW * 64),
                        lds, stream, p);
+    return hipGetLastError();
+}
+
+// ---- fused mixed step ------------------------------------------------------
+//
+// A scheduler step that carries decodes and prefill chunks together
+// (src/scheduler.h:14-23; the engine serves them in one step,
+// src/paged_engine.cpp:254-269) as one launch (opt-in; vcpp_paged_mixed_step
+// runs two launches by default, which measured faster).  Decode is HBM-bound
+// and prefill MFMA-bound, so the launch puts both on every CU at once: three
+// 4-wave workgroups per CU (168 VGPRs, 3 waves per SIMD), one of them a
+// decode worker walking the balanced split with 4 kv heads
+// (decode_page_body), two of them prefill workers taking query tiles of 32
+// rows (prefill_tile, heaviest tiles first) in a fixed stride.  Workgroups
+// are dealt to the 8 XCDs by linear id, and within an XCD the roles repeat
+// every three workgroups, so with the launch sized to three per CU each CU
+// holds one decode and two prefill workers whatever order the CUs are filled
+// in.
+constexpr int kMixedWpc = 3;    // workgroups per CU
+constexpr int kMixedPrefill = 2;  // of them prefill workers
+struct MixedGrid {
+    int pf_items;  // prefill work items: tiles x chunks x (kv head, head group)
+    int pf_nyz;    // chunks x (kv head, head group)
+    int pf_nz;     // (kv head, head group) pairs
+    int dec_hg;    // kv-head groups of 4 (decode workgroups per range)
+};
+
+template <int KV, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kMixedWpc, kMixedWpc)))
+void mixed_step_kernel(DecodeParams dp, PrefillParams pp, MixedGrid mg) {
+    constexpr int W = kMixedWpc, NPF = kMixedPrefill, NDEC = W - NPF;
+    const int id = blockIdx.x, xcd = id & 7, local = id >> 3;
+    const int per_cu = (gridDim.x >> 3) / W;  // CUs per XCD
+    const int trip = local / W, role = local - W * trip;
+    if (role >= NDEC) {
+        extern __shared__ __attribute__((aligned(16))) char smem[];
+        lds_char* lds = reinterpret_cast<lds_char*>((__attribute__((address_space(3))) char*)smem);
+        const int workers = NPF * (gridDim.x / W);
+        for (int it = xcd * NPF * per_cu + NPF * trip + role - NDEC; it < mg.pf_items; it += workers) {
+            const int bx = it / mg.pf_nyz, r = it - bx * mg.pf_nyz;
+            const int by = r / mg.pf_nz, bz = r - by * mg.pf_nz;
+            prefill_tile<KV, D, true>(pp, bx, by, bz, lds);
+            __syncthreads();  // the next item reuses the LDS
+        }
+    } else {
+        // decode worker 0 .. NDEC CUs - 1, the head groups of one range adjacent
+        const int di = xcd * NDEC * per_cu + NDEC * trip + role;
+        const int bx = di / mg.dec_hg, by = di - bx * mg.dec_hg;
+        if (bx < dp.page_grid) decode_page_body<KV, D, 4, true>(dp, bx, by, dp.page_grid);
+    }
+}
+
+template <int KV, int D>
+size_t mixed_lds(int max_blocks) {
+    constexpr bool BYTES = KV != VCPP_KV_F16;
+    constexpr size_t pf = BYTES ? (size_t)ByteDims<D, KV == VCPP_KV_I8, true>::STAGES *
+                                          ByteDims<D, KV == VCPP_KV_I8, true>::STAGE +
+                                      2 * (size_t)DmaDims<D, true>::STAGE
+                                : (size_t)DmaDims<D, true>::STAGES * DmaDims<D, true>::STAGE;
+    return std::max<size_t>(PageCfg<KV, D, 4, true>::LDS, pf + (size_t)max_blocks * 4);
+}
+
+template <int KV, int D>
+hipError_t launch_mixed_kd(const DecodeParams& dp, const PrefillParams& pp, int cus, hipStream_t stream) {
+    const size_t lds = mixed_lds<KV, D>(pp.max_blocks);
+    static bool attr_set[64] = {};
+    int dev = 0;
+    if (lds > 65536 && (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || !attr_set[dev])) {
+        const hipError_t e = hipFuncSetAttribute((const void*)mixed_step_kernel<KV, D>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 160 * 1024 / kMixedWpc);
+        if (e != hipSuccess) return e;
+        if (dev >= 0 && dev < 64) attr_set[dev] = true;
+    }
+    MixedGrid mg;
+    constexpr int QT = 16 * PDims<D, true>::RB;
+    mg.pf_nz = pp.num_kv_heads * pp.head_groups;
+    mg.pf_nyz = pp.num_chunks * mg.pf_nz;
+    mg.pf_items = (pp.max_chunk_len + QT - 1) / QT * mg.pf_nyz;
+    mg.dec_hg = dp.num_kv_heads / 4;
+    hipLaunchKernelGGL((mixed_step_kernel<KV, D>), dim3(kMixedWpc * cus), dim3(256), lds, stream, dp, pp, mg);
     return hipGetLastError();
 }
 
@@ -1596,6 +1689,49 @@ bool decode_page_mode_supported(int kv_dtype, int num_kv_heads, int group, int h
 bool decode_head_dim_supported(int kv_dtype, int head_dim) {
     if (kv_dtype == VCPP_KV_F32) return head_dim > 0 && head_dim <= 256 && head_dim % 4 == 0;
     return head_dim == 64 || head_dim == 80 || head_dim == 128;
+}
+
+int mixed_decode_grid(int kv_dtype, int num_kv_heads, int group, int head_dim, int block_size, int cus) {
+    if (kv_dtype != VCPP_KV_F16 && kv_dtype != VCPP_KV_I8 && kv_dtype != VCPP_KV_FP8) return 0;
+    if ((head_dim != 64 && head_dim != 80) || num_kv_heads % 4 != 0 || group > 8 || block_size % kTile != 0)
+        return 0;
+    const int hg = num_kv_heads / 4;
+    const int ndec = kMixedWpc - kMixedPrefill;
+    if (cus <= 0 || cus % 8 != 0 || (ndec * cus / 8) % hg != 0) return 0;
+    return ndec * cus / hg;
+}
+
+size_t mixed_lds_bytes(int kv_dtype, int head_dim, int max_blocks) {
+#define VCPP_MIXED_LDS(KVT) (head_dim == 64 ? mixed_lds<KVT, 64>(max_blocks) : mixed_lds<KVT, 80>(max_blocks))
+    if (kv_dtype == VCPP_KV_I8) return VCPP_MIXED_LDS(VCPP_KV_I8);
+    if (kv_dtype == VCPP_KV_FP8) return VCPP_MIXED_LDS(VCPP_KV_FP8);
+    return VCPP_MIXED_LDS(VCPP_KV_F16);
+#undef VCPP_MIXED_LDS
+}
+
+hipError_t launch_mixed(const DecodeParams& dp, const PrefillParams& pp, int cus, hipStream_t stream) {
+    hipError_t err;
+    const bool prof = prof_enabled();
+    if (prof) prof_begin(kKernelMixed, stream);
+#define VCPP_MIXED_D(KVT)                                                                          \
+    err = dp.head_dim == 64 ? launch_mixed_kd<KVT, 64>(dp, pp, cus, stream) : launch_mixed_kd<KVT, 80>(dp, pp, cus, stream);
+    if (dp.kv_dtype == VCPP_KV_I8) {
+        VCPP_MIXED_D(VCPP_KV_I8)
+    } else if (dp.kv_dtype == VCPP_KV_FP8) {
+        VCPP_MIXED_D(VCPP_KV_FP8)
+    } else {
+        VCPP_MIXED_D(VCPP_KV_F16)
+    }
+#undef VCPP_MIXED_D
+    if (err != hipSuccess) return err;
+    if (prof) prof_end(kKernelMixed, stream);
+    if (prof) prof_begin(kKernelMerge, stream);
+    dim3 mgr(dp.num_seqs, (dp.pairs + 3) / 4);
+    if (dp.head_dim == 64) hipLaunchKernelGGL(merge_split_kernel<64>, mgr, dim3(256), 0, stream, dp);
+    else hipLaunchKernelGGL(merge_split_kernel<80>, mgr, dim3(256), 0, stream, dp);
+    err = hipGetLastError();
+    if (prof) prof_end(kKernelMerge, stream);
+    return err;
 }
 
 }  // namespace vcpp

@@ -5,7 +5,7 @@
 
 namespace vcpp {
 
-enum KernelId { kKernelDecode = 0, kKernelMerge = 1, kKernelPrefill = 2, kKernelCount = 3 };
+enum KernelId { kKernelDecode = 0, kKernelMerge = 1, kKernelPrefill = 2, kKernelMixed = 3, kKernelCount = 4 };
 
 // True while vcpp_profile_enable(1) is in force.
 bool prof_enabled();

@@ -43,7 +43,7 @@ EXPORTS = [
     "vcpp_profile_read",
 ]
 
-KERNEL_DECODE, KERNEL_MERGE, KERNEL_PREFILL = 0, 1, 2
+KERNEL_DECODE, KERNEL_MERGE, KERNEL_PREFILL, KERNEL_MIXED = 0, 1, 2, 3
 
 
 class KVPages(ctypes.Structure):
@@ -107,6 +107,11 @@ def open_library(path):
     L.vcpp_paged_prefill.argtypes = [ctypes.POINTER(KVPages), vp, vp, vp, i32, vp, vp, i32, i32,
                                      i32, vp]
     L.vcpp_paged_prefill.restype = ctypes.c_int
+    L.vcpp_paged_mixed_step.argtypes = [ctypes.POINTER(KVPages), vp, vp, vp, i32, vp, vp, i32, i32,
+                                        vp, vp, vp, i32, vp, vp, i32, i32, i32, vp, sz, vp]
+    L.vcpp_paged_mixed_step.restype = ctypes.c_int
+    L.vcpp_mixed_workspace_size.argtypes = [ctypes.POINTER(KVPages), i32, i32, i32, i32]
+    L.vcpp_mixed_workspace_size.restype = sz
     L.vcpp_write_kv.argtypes = [ctypes.POINTER(KVPages), vp, vp, vp, i32, i32, vp]
     L.vcpp_write_kv.restype = ctypes.c_int
     L.vcpp_qk_norm_rope.argtypes = [vp, vp, i32, i32, i32, i32, vp, vp, ctypes.c_float, vp, vp,
@@ -222,6 +227,33 @@ def paged_prefill(pages, q, out, block_tables, q_start, prefix_lens, max_chunk_l
                                   prefix_lens.shape[0], max_chunk_len, num_heads, _stream(stream))
     _check(rc)
     return out
+
+
+def mixed_workspace_size(pages, num_seqs, num_heads, max_context_len, max_blocks_per_chunk):
+    return lib().vcpp_mixed_workspace_size(ctypes.byref(pages), num_seqs, num_heads, max_context_len,
+                                           max_blocks_per_chunk)
+
+
+def paged_mixed_step(pages, dq, dout, d_tables, context_lens, max_context_len, pq, pout, p_tables,
+                     q_start, prefix_lens, max_chunk_len, num_heads, d_table_lens=None,
+                     workspace=None, stream=None):
+    """vcpp_paged_mixed_step: a decode batch (dq fp32 [S][H][D]) and prefill
+    chunks (pq fp16 [rows][H][D]) over the same pages in one step."""
+    num_seqs = dq.shape[0] if dq is not None else 0
+    num_chunks = prefix_lens.shape[0] if prefix_lens is not None else 0
+    dmb = d_tables.shape[1] if d_tables is not None and d_tables.dim() == 2 else 0
+    pmb = p_tables.shape[1] if p_tables is not None and p_tables.dim() == 2 else 0
+    need = mixed_workspace_size(pages, num_seqs, num_heads, max_context_len, pmb)
+    if workspace is None and need > 0:
+        import torch
+        workspace = torch.zeros(need, dtype=torch.uint8, device=dq.device)
+    ws_bytes = workspace.numel() if workspace is not None else 0
+    rc = lib().vcpp_paged_mixed_step(ctypes.byref(pages), _ptr(dq), _ptr(dout), _ptr(d_tables), dmb,
+                                     _ptr(d_table_lens), _ptr(context_lens), num_seqs, max_context_len,
+                                     _ptr(pq), _ptr(pout), _ptr(p_tables), pmb, _ptr(q_start),
+                                     _ptr(prefix_lens), num_chunks, max_chunk_len, num_heads,
+                                     _ptr(workspace), ws_bytes, _stream(stream))
+    _check(rc)
 
 
 def write_kv(pages, k, v, slots, fp16_round_nearest=False, stream=None):
