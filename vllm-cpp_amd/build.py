@@ -14,7 +14,7 @@ ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libvcpp_attn.so")
 SOURCES = ["csrc/decode.hip", "csrc/prefill.hip", "csrc/dense.hip", "csrc/kv_write.hip", "csrc/qk_prep.hip", "csrc/api.cpp",
            "csrc/profile.cpp", "csrc/noalloc.cpp", "host/kv_cache_manager.cpp", "host/paged_attention.cpp"]
-HEADERS = ["host/host_util.h", "csrc/decode.h", "csrc/prefill.h", "csrc/dense.h", "csrc/kv_write.h", "csrc/qk_prep.h", "csrc/device_common.h", "csrc/profile.h"]
+HEADERS = ["host/host_util.h", "csrc/decode.h", "csrc/prefill.h", "csrc/prefill_body.h", "csrc/dense.h", "csrc/kv_write.h", "csrc/qk_prep.h", "csrc/device_common.h", "csrc/profile.h"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -64,6 +64,11 @@ namespace vcpp {
 namespace {
 
 constexpr int kTile = 16;          // tokens per MFMA tile
+// Page-staged decode's lazy running max (log2 units): the max moves when a
+// tile's scores pass it by more than kPageLazy, and is looked at only when a
+// lane's sum of P over its 4 tokens passes kPageLazySum.
+constexpr float kPageLazy = 8.0f;
+constexpr float kPageLazySum = 1024.0f;
 // Pipeline shape (template parameters of the kernel): TPS tiles per step
 // (one softmax update), NBUF register buffers, loads issued NBUF-1 steps ahead.
 // Waves (kv heads) per workgroup: 4 kv heads x 80 dims x 2 B = 640 B, five
@@ -1261,6 +1266,7 @@ __device__ __forceinline__ void decode_page_body(const DecodeParams& p, int bx, 
     typedef __attribute__((address_space(3))) uint32_t lds_u32;
     typedef __attribute__((address_space(3))) i2 lds_i2;
 
+    const float lo_sel = c < 8 ? 0.f : -1.f;
     auto compute_tile = [&](int tau, const PageEntry& e) {
         lds_char* sb = lds + (tau % STAGES) * STAGE;
         const int pos0 = e.tis * kTile;
@@ -1296,8 +1302,10 @@ __device__ __forceinline__ void decode_page_body(const DecodeParams& p, int bx, 
                 acc += mfma16(kf, qr, zero);
             }
         }
+        // Visible tokens of the tile (uniform): all 16, the sequence's
+        // remainder, or none on a missing page.
+        const int lim = full ? kTile : (e.bid >= 0 ? cur_end - pos0 : 0);
         float sc[4];
-        float mx = kMaxSeed;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             float x = acc[r] + dpp_ror8(acc[r]);
@@ -1307,36 +1315,59 @@ __device__ __forceinline__ void decode_page_body(const DecodeParams& p, int bx, 
                 f *= h_to_f((r & 1) ? (wd >> 16) : (wd & 0xFFFFu));
             }
             x *= f;
-            if (!full) x = (e.bid >= 0 && pos0 + 4 * g + r < cur_end) ? x : -__builtin_inff();
-            sc[r] = x;
-            mx = fmaxf(mx, x);
+            sc[r] = 4 * g + r < lim ? x : -__builtin_inff();
         }
-        mx = fmaxf(mx, shfl_xor(mx, 16));
-        mx = fmaxf(mx, shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = fast_exp2(m_run - m_new);
-        m_run = m_new;
-        if (__any(alpha != 1.0f)) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float al = shfl(alpha, (4 * g + r) & 7);
-#pragma unroll
-                for (int t = 0; t < NT; ++t) o[t][r] *= al;
-            }
-        }
-        float lsum = 0.f;
-        h4 pa;
+        // Lazy running max: P against the current max; only when a lane's
+        // sum of P passes 2^10 (so some P may exceed it, or is inf / NaN)
+        // is the tile's max formed, and the max moves when it grows by more
+        // than 2^kPageLazy -- so P stays <= 2^10 (fp16 hi/lo split exact to
+        // ~22 bits) and most tiles need no cross-lane reduction.
+        float pr[4], lsum = 0.f;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            float pr = fast_exp2(sc[r] - m_new);
-            lsum += pr;
-            if constexpr (SCALED) {
+            pr[r] = fast_exp2(sc[r] - m_run);
+            lsum += pr[r];
+        }
+        if (__builtin_expect(__any(!(lsum <= kPageLazySum)), 0)) {
+            float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+            mx = fmaxf(mx, shfl_xor(mx, 16));
+            mx = fmaxf(mx, shfl_xor(mx, 32));
+            const bool grow = mx > m_run + kPageLazy;
+            const float m_new = grow ? mx : m_run;
+            const float alpha = fast_exp2(m_run - m_new);
+            m_run = m_new;
+            if (__any(alpha != 1.0f)) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float al = shfl(alpha, (4 * g + r) & 7);
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) o[t][r] *= al;
+                }
+            }
+            l_run *= alpha;
+            lsum = 0.f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                pr[r] = fast_exp2(sc[r] - m_run);
+                lsum += pr[r];
+            }
+        }
+        if constexpr (SCALED) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
                 const uint32_t wd = (uint32_t)(r < 2 ? vsw.x : vsw.y);
                 // masked tokens have pr == 0; the select keeps 0 * garbage out
-                pr = pr > 0.f ? pr * h_to_f((r & 1) ? (wd >> 16) : (wd & 0xFFFFu)) : 0.f;
+                pr[r] = pr[r] > 0.f ? pr[r] * h_to_f((r & 1) ? (wd >> 16) : (wd & 0xFFFFu)) : 0.f;
             }
-            const _Float16 hi = (_Float16)pr;
-            pa[r] = c < 8 ? hi : (_Float16)(pr - (float)hi);
+        }
+        // Rows 0-7 carry fp16(p), rows 8-15 p - fp16(p): x = p - lo_sel * fp16(p).
+        h4 pa;
+#pragma unroll
+        for (int r = 0; r < 4; r += 2) {
+            const h2 hi = {(_Float16)pr[r], (_Float16)pr[r + 1]};
+            const float x0 = fmaf(lo_sel, (float)hi[0], pr[r]), x1 = fmaf(lo_sel, (float)hi[1], pr[r + 1]);
+            pa[r] = (_Float16)x0;
+            pa[r + 1] = (_Float16)x1;
         }
         if constexpr (BYTES) {
             // One ds_read_b64_tr_b8 per pair of output blocks (t, t+1): lane
@@ -1363,7 +1394,7 @@ __device__ __forceinline__ void decode_page_body(const DecodeParams& p, int bx, 
                 o[t] = mfma16(pa, __builtin_bit_cast(h4, x), o[t]);
             }
         }
-        l_run = l_run * alpha + lsum;
+        l_run += lsum;
     };
 
     for (int win0 = a; win0 < b; win0 += kPageWindow) {
