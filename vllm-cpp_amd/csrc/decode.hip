@@ -1302,6 +1302,31 @@ __device__ __forceinline__ void decode_page_body(const DecodeParams& p, int bx, 
                 acc += mfma16(kf, qr, zero);
             }
         }
+        // V operands, read here so that their LDS latency overlaps the S
+        // MFMAs and the softmax.  Byte pages: one ds_read_b64_tr_b8 per pair
+        // of output blocks (t, t+1): lane i of each 16-lane group gets byte
+        // i mod 8 of the read of lane 2j + i/8, j = 0..7.  Lanes 2j, 2j+1 of
+        // group g read token 4g + (j & 3), dims 16u .. 16u+15 of head kvh
+        // (one 16-byte chunk), u = t for j < 4 and t+1 above, so lane (g, c)
+        // gets V[4g + r][16t + c] in bytes r and V[4g + r][16(t+1) + c] in
+        // bytes 4 + r.  An odd last block reads itself twice.  fp16 pages:
+        // one ds_read_b64_tr_b16 per output block.
+        i2 vx[BYTES ? (NT + 1) / 2 : 1];
+        s4 vh[BYTES ? 1 : NT];
+        if constexpr (BYTES) {
+#pragma unroll
+            for (int t = 0; t < NT; t += 2) {
+                const int j = c >> 1;
+                const int u = (j < 4 || t + 1 == NT) ? t : t + 1;
+                const int ofs = REG + page_slot<SWZ>((4 * g + (j & 3)) * RC + wave * HC + u, RC) * 16 + 8 * (c & 1);
+                vx[t / 2] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(reinterpret_cast<lds_i2*>(sb + ofs));
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                vh[t] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    reinterpret_cast<__attribute__((address_space(3))) s4*>(sb + vofs(t)));
+        }
         // Visible tokens of the tile (uniform): all 16, the sequence's
         // remainder, or none on a missing page.
         const int lim = full ? kTile : (e.bid >= 0 ? cur_end - pos0 : 0);
@@ -1370,29 +1395,14 @@ __device__ __forceinline__ void decode_page_body(const DecodeParams& p, int bx, 
             pa[r + 1] = (_Float16)x1;
         }
         if constexpr (BYTES) {
-            // One ds_read_b64_tr_b8 per pair of output blocks (t, t+1): lane
-            // i of each 16-lane group gets byte i mod 8 of the read of lane
-            // 2j + i/8, j = 0..7.  Lanes 2j, 2j+1 of group g read token
-            // 4g + (j & 3), dims 16u .. 16u+15 of head kvh (one 16-byte
-            // chunk), u = t for j < 4 and t+1 above, so lane (g, c) gets
-            // V[4g + r][16t + c] in bytes r and V[4g + r][16(t+1) + c] in
-            // bytes 4 + r.  An odd last block reads itself twice.
 #pragma unroll
             for (int t = 0; t < NT; t += 2) {
-                const int j = c >> 1;
-                const int u = (j < 4 || t + 1 == NT) ? t : t + 1;
-                const int ofs = REG + page_slot<SWZ>((4 * g + (j & 3)) * RC + wave * HC + u, RC) * 16 + 8 * (c & 1);
-                const i2 x = __builtin_amdgcn_ds_read_tr8_b64_v2i32(reinterpret_cast<lds_i2*>(sb + ofs));
-                o[t] = mfma16(pa, bytes4_to_h4<KV>((uint32_t)x.x), o[t]);
-                if (t + 1 < NT) o[t + 1] = mfma16(pa, bytes4_to_h4<KV>((uint32_t)x.y), o[t + 1]);
+                o[t] = mfma16(pa, bytes4_to_h4<KV>((uint32_t)vx[t / 2].x), o[t]);
+                if (t + 1 < NT) o[t + 1] = mfma16(pa, bytes4_to_h4<KV>((uint32_t)vx[t / 2].y), o[t + 1]);
             }
         } else {
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const s4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    reinterpret_cast<__attribute__((address_space(3))) s4*>(sb + vofs(t)));
-                o[t] = mfma16(pa, __builtin_bit_cast(h4, x), o[t]);
-            }
+            for (int t = 0; t < NT; ++t) o[t] = mfma16(pa, __builtin_bit_cast(h4, vh[t]), o[t]);
         }
         l_run += lsum;
     };
