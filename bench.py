@@ -53,7 +53,7 @@ def parse():
     ap.add_argument("--c4-partitions", type=lambda x: [int(v) for v in x.split(",")],
                     default=[256, 0], help="config 4 variants: partition sizes (0 = balanced)")
     ap.add_argument("--only", choices=["decode", "prefill", "config1", "config4", "config5", "qkprep", "fp8",
-                                       "kvwrite", "dense"],
+                                       "kvwrite", "dense", "longprefill"],
                     help="run one leg only and print its JSON (for profiling)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the prefill leg (for profiling its kernel)")
@@ -343,6 +343,44 @@ def bench_config5(torch, pyvcpp, args):
             "config": {"workload": "BASELINE config 5: 128 decode seqs ctx U[1024,8192] + 4 prefill "
                                    "chunks x 512 on 1024-token prefixes, int8 KV + fp16 scales, GQA 8:1, "
                                    "head_dim 80", "decode_bytes": dbytes, "prefill_flops": flops}}
+
+
+def bench_long_prefill(torch, pyvcpp, args):
+    """Chunked prefill of one long request: one chunk of 512 new tokens on a
+    paged prefix of 8K / 32K tokens (64 q / 8 kv heads, head_dim 80, fp16
+    pages).  The grid of the unsplit kernel is 128 workgroups on 256 CUs;
+    vcpp_paged_prefill_split cuts each tile's keys over several workgroups."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(args.seed + 60)
+    gd = torch.Generator(device=dev).manual_seed(args.seed + 61)
+    res = {}
+    for prefix_len in (8192, 32768):
+        lens = [prefix_len + 512]
+        nb = math.ceil(1.25 * lens[0] / BS)
+        k = torch.randn((nb, BS, HKV, D), generator=gd, device=dev, dtype=torch.float16)
+        v = torch.randn((nb, BS, HKV, D), generator=gd, device=dev, dtype=torch.float16)
+        pages = pyvcpp.kv_pages(pyvcpp.KV_F16, k, v, BS, HKV, D, nb, BS * HKV * D)
+        tables, _ = random_tables(torch, g, lens, nb, dev)
+        q = torch.randn((512, H, D), generator=gd, device=dev).half().view(torch.int16)
+        out = torch.empty((512, H, D), dtype=torch.float32, device=dev)
+        q_start = torch.tensor([0, 512], dtype=torch.int32, device=dev)
+        prefix = torch.tensor([prefix_len], dtype=torch.int32, device=dev)
+        need = pyvcpp.prefill_workspace_size(pages, 1, 512, prefix_len, H)
+        ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=dev)
+        flops = 4 * D * H * sum(prefix_len + i + 1 for i in range(512))
+        row = {}
+        for name, fn in (("unsplit", lambda: pyvcpp.paged_prefill(pages, q, out, tables, q_start, prefix, 512, H)),
+                         ("split", lambda: pyvcpp.paged_prefill_split(pages, q, out, tables, q_start, prefix,
+                                                                      512, prefix_len, H, workspace=ws))):
+            dt = timed(torch, fn, args.config_steps)
+            row[name] = {"us_per_call": round(dt * 1e6, 1), "TFLOP/s": round(flops / dt / 1e12, 1)}
+        row["workspace_bytes"] = need
+        res["512_on_%d" % prefix_len] = row
+    return {"metric": "long-prefix chunked prefill TFLOP/s (split vs unsplit)", "unit": "TFLOP/s",
+            "value": res["512_on_32768"]["split"]["TFLOP/s"], "variants": res,
+            "steps": args.config_steps,
+            "config": {"workload": "1 chunk x 512 new tokens on an 8K / 32K paged prefix, 64 q / 8 kv "
+                                   "heads, head_dim 80, fp16 pages"}}
 
 
 # ---------------------------------------------------------------------------
@@ -704,6 +742,9 @@ def main():
     if args.only == "dense":
         print(json.dumps(bench_dense(torch, pyvcpp, args)))
         return
+    if args.only == "longprefill":
+        print(json.dumps(bench_long_prefill(torch, pyvcpp, args)))
+        return
 
     w = decode_workload(torch, args.seed)
     pages0 = pyvcpp.kv_pages(pyvcpp.KV_F16, w["sets"][0][0], w["sets"][0][1], BS, HKV, D, w["nb"],
@@ -764,6 +805,7 @@ def main():
     if not args.no_configs:
         result["config4"] = bench_config4(torch, pyvcpp, args)
         result["config5"] = bench_config5(torch, pyvcpp, args)
+        result["long_prefill"] = bench_long_prefill(torch, pyvcpp, args)
         result["qk_prep"] = bench_qkprep(torch, pyvcpp, args)
         result["fp8_decode"] = bench_fp8(torch, pyvcpp, args)
         result["kv_write"] = bench_kvwrite(torch, pyvcpp, args)

@@ -180,6 +180,28 @@ int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
                        const int32_t* q_start, const int32_t* prefix_lens, int32_t num_chunks,
                        int32_t max_chunk_len, int32_t num_heads, void* stream);
 
+/*
+ * vcpp_paged_prefill with the keys of each query tile split over several
+ * workgroups when the chunks alone would leave the GPU under-filled (few
+ * chunks on long prefixes, e.g. chunked prefill of one long request): each
+ * part leaves unnormalised outputs and (max, sum) in the workspace and a
+ * log-sum-exp merge writes `out`.  Same arguments and results as
+ * vcpp_paged_prefill, plus
+ *   max_prefix_len  host-side upper bound of prefix_lens (sizes the split)
+ *   workspace       device scratch of at least vcpp_prefill_workspace_size(...)
+ *                   bytes (none needed when that is 0)
+ * Calls on one stream may share a workspace; calls that overlap may not.
+ * No reference counterpart: the reference prefills one position at a time
+ * (src/paged_engine.cpp:381-384).
+ */
+int vcpp_paged_prefill_split(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
+                             const int32_t* block_tables, int32_t max_blocks_per_seq, const int32_t* q_start,
+                             const int32_t* prefix_lens, int32_t num_chunks, int32_t max_chunk_len,
+                             int32_t max_prefix_len, int32_t num_heads, void* workspace, size_t workspace_bytes,
+                             void* stream);
+size_t vcpp_prefill_workspace_size(const vcpp_kv_pages* kv, int32_t num_chunks, int32_t max_chunk_len,
+                                   int32_t max_prefix_len, int32_t num_heads);
+
 /* ---- v2: one scheduler step with decodes and prefill chunks ------------- */
 
 /*

@@ -102,3 +102,18 @@ def oracle_prefill_rows(pool, q32, tables, q_start, prefix, num_heads, rows, nth
     chunk_of = np.searchsorted(q_start, rows, side="right") - 1
     ctx = np.array([prefix[c] + (r - q_start[c]) + 1 for r, c in zip(rows, chunk_of)], np.int32)
     return decode(pool, q32[rows], tables[chunk_of], ctx, num_heads, nthreads=nthreads)
+
+
+def gpu_prefill_split(dpool, q16, tables, q_start, prefix, num_heads, workspace=None):
+    """vcpp_paged_prefill_split; returns (out, splits used > 1)."""
+    qd = dev(q16)
+    out = torch.full(q16.shape, float("nan"), dtype=torch.float32, device="cuda:0")
+    lens = np.diff(q_start)
+    mcl = int(lens.max()) if len(lens) else 0
+    mpl = int(np.max(prefix)) if len(prefix) else 0
+    need = pyvcpp.prefill_workspace_size(dpool.pages, len(lens), mcl, mpl, num_heads)
+    pyvcpp.paged_prefill_split(dpool.pages, qd, out, dev(np.asarray(tables, np.int32)),
+                               dev(np.asarray(q_start, np.int32)), dev(np.asarray(prefix, np.int32)),
+                               mcl, mpl, num_heads, workspace=workspace)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), need > 0

@@ -489,6 +489,8 @@ vcpp::PrefillParams prefill_params(const vcpp_kv_pages* kv, const uint16_t* q, f
     p.max_chunk_len = max_chunk_len;
     p.scale_log2 = (1.0f / std::sqrt((float)kv->head_dim)) * 1.4426950408889634f;
     p.bs_magic = ((1ull << 40) + kv->block_size - 1) / kv->block_size;
+    p.splits = 1;
+    p.rows_cap = (int32_t)std::min<int64_t>((int64_t)num_chunks * max_chunk_len, INT32_MAX);
 #ifdef VCPP_GATHER_DUMP
     p.gather_dump = g_gather_dump;
     p.gather_stride = g_gather_stride;
@@ -553,6 +555,59 @@ int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
     if (rc != VCPP_OK || num_chunks == 0 || max_chunk_len == 0) return rc;
     const vcpp::PrefillParams p = prefill_params(kv, q, out, block_tables, max_blocks_per_seq, q_start,
                                                  prefix_lens, num_chunks, max_chunk_len, num_heads);
+    hipError_t e = vcpp::launch_prefill(p, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "prefill launch");
+    return VCPP_OK;
+}
+
+// Key parts of a split prefill: enough workgroups to fill two per CU, each
+// part at least 16 key blocks (512 keys) of the longest chunk, at most 16.
+static int32_t prefill_splits(const vcpp_kv_pages* kv, int32_t num_chunks, int32_t max_chunk_len,
+                              int32_t max_prefix_len, int32_t num_heads) {
+    if (num_chunks <= 0 || max_chunk_len <= 0 || max_prefix_len < 0) return 1;
+    const int64_t qt = kv->head_dim <= 80 ? 64 : 32;  // query rows per workgroup
+    const int64_t items = (max_chunk_len + qt - 1) / qt * num_chunks * kv->num_kv_heads *
+                          vcpp::prefill_head_groups(num_heads / kv->num_kv_heads);
+    const int64_t slots = 2 * (int64_t)device_cus();
+    if (items >= slots) return 1;
+    const int64_t want = (slots + items - 1) / items;
+    const int64_t by_len = ((int64_t)max_prefix_len + max_chunk_len) / (16 * 32);
+    return (int32_t)std::max<int64_t>(1, std::min<int64_t>({want, by_len, 16}));
+}
+
+size_t vcpp_prefill_workspace_size(const vcpp_kv_pages* kv, int32_t num_chunks, int32_t max_chunk_len,
+                                   int32_t max_prefix_len, int32_t num_heads) {
+    if (!kv || kv->num_kv_heads <= 0 || num_heads <= 0 || num_heads % kv->num_kv_heads != 0) return 0;
+    const int32_t s = prefill_splits(kv, num_chunks, max_chunk_len, max_prefix_len, num_heads);
+    return vcpp::prefill_split_bytes(s, (int32_t)std::min<int64_t>((int64_t)num_chunks * max_chunk_len, INT32_MAX),
+                                     num_heads, kv->head_dim);
+}
+
+int vcpp_paged_prefill_split(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
+                             const int32_t* block_tables, int32_t max_blocks_per_seq, const int32_t* q_start,
+                             const int32_t* prefix_lens, int32_t num_chunks, int32_t max_chunk_len,
+                             int32_t max_prefix_len, int32_t num_heads, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+    g_last_error.clear();
+    int rc = check_prefill(kv, q, out, block_tables, max_blocks_per_seq, q_start, prefix_lens, num_chunks,
+                           max_chunk_len, num_heads);
+    if (rc != VCPP_OK || num_chunks == 0 || max_chunk_len == 0) return rc;
+    if (max_prefix_len < 0) return fail(VCPP_E_INVALID, "max_prefix_len must be >= 0");
+    vcpp::PrefillParams p = prefill_params(kv, q, out, block_tables, max_blocks_per_seq, q_start, prefix_lens,
+                                           num_chunks, max_chunk_len, num_heads);
+    p.splits = prefill_splits(kv, num_chunks, max_chunk_len, max_prefix_len, num_heads);
+    if ((int64_t)kv->num_kv_heads * p.head_groups * p.splits > 65535)
+        return fail(VCPP_E_UNSUPPORTED, "too many heads x key parts");
+    if (p.splits > 1) {
+        const size_t need = vcpp::prefill_split_bytes(p.splits, p.rows_cap, num_heads, kv->head_dim);
+        if (!workspace || workspace_bytes < need)
+            return fail(VCPP_E_WORKSPACE, "split prefill needs %zu workspace bytes, got %zu", need,
+                        workspace ? workspace_bytes : (size_t)0);
+        const size_t rows = (size_t)p.splits * p.rows_cap * num_heads;
+        p.ws_o = static_cast<float*>(workspace);
+        p.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) +
+                                            ((rows * kv->head_dim * sizeof(float) + 255) & ~size_t(255)));
+    }
     hipError_t e = vcpp::launch_prefill(p, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "prefill launch");
     return VCPP_OK;

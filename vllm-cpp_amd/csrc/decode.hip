@@ -1546,7 +1546,7 @@ void mixed_step_kernel(DecodeParams dp, PrefillParams pp, MixedGrid mg) {
         for (int it = xcd * NPF * per_cu + NPF * trip + role - NDEC; it < mg.pf_items; it += workers) {
             const int bx = it / mg.pf_nyz, r = it - bx * mg.pf_nyz;
             const int by = r / mg.pf_nz, bz = r - by * mg.pf_nz;
-            prefill_tile<KV, D, true>(pp, bx, by, bz, lds);
+            prefill_tile<KV, D, true>(pp, bx, by, bz, 0, lds);
             __syncthreads();  // the next item reuses the LDS
         }
     } else {

@@ -35,6 +35,13 @@ struct PrefillParams {
     int32_t num_chunks;
     int32_t max_chunk_len;
     float scale_log2;  // log2(e) / sqrt(head_dim)
+    // split-K over the keys (1: none): part k of a tile's key blocks leaves
+    // unnormalised outputs and (max, sum) in ws_o / ws_ml at row
+    // k * rows_cap + row, for launch_prefill's merge
+    int32_t splits;
+    int32_t rows_cap;  // >= the rows of all chunks (num_chunks * max_chunk_len)
+    float* ws_o;       // [splits][rows_cap][num_heads][head_dim]
+    float2* ws_ml;     // [splits][rows_cap][num_heads] (max in log2 units, sum)
     uint64_t bs_magic; // ceil(2^40 / block_size): pos / block_size = (pos * bs_magic) >> 40
 #ifdef VCPP_GATHER_DUMP
     int32_t* gather_dump;    // checker builds: [rows][gather_stride][2] (block, slot)
@@ -43,6 +50,8 @@ struct PrefillParams {
 };
 
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream);
+// Workspace bytes of a split prefill (0 when splits <= 1).
+size_t prefill_split_bytes(int splits, int rows_cap, int num_heads, int head_dim);
 int prefill_head_groups(int group);
 // Dynamic LDS bytes of the prefill kernel for a table of max_blocks entries.
 size_t prefill_lds_bytes(int kv_dtype, int head_dim, int max_blocks);

@@ -25,15 +25,48 @@ void prefill_dma_kernel(PrefillParams p) {
         by = (m / nx) % ny;
         bz = m / (nx * ny);
     }
-    prefill_tile<KV, D, false>(p, bx, by, bz,
+    // z: (key part, kv head, head group)
+    const int zh = p.num_kv_heads * p.head_groups;
+    const int part = bz / zh;
+    prefill_tile<KV, D, false>(p, bx, by, bz - part * zh, part,
                                reinterpret_cast<lds_char*>((__attribute__((address_space(3))) char*)smem));
+}
+
+// Log-sum-exp merge of a split prefill's parts: thread (row, head, 4 dims).
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
+    const int D4 = p.head_dim / 4;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t per_row = (int64_t)p.num_heads * D4;
+    const int row = (int)(idx / per_row);
+    if (row >= p.q_start[p.num_chunks]) return;
+    const int rem = (int)(idx - row * per_row);
+    const int head = rem / D4, d4 = rem - head * D4;
+    float M = -__builtin_inff();
+    for (int s = 0; s < p.splits; ++s)
+        M = fmaxf(M, p.ws_ml[((int64_t)s * p.rows_cap + row) * p.num_heads + head].x);
+    float L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < p.splits; ++s) {
+        const int64_t rh = ((int64_t)s * p.rows_cap + row) * p.num_heads + head;
+        const float2 ml = p.ws_ml[rh];
+        const float w = ml.y > 0.f ? exp2f(ml.x - M) : 0.f;  // empty parts weigh 0
+        L += w * ml.y;
+        const float4 v = reinterpret_cast<const float4*>(p.ws_o + rh * p.head_dim)[d4];
+        acc.x += w * v.x;
+        acc.y += w * v.y;
+        acc.z += w * v.z;
+        acc.w += w * v.w;
+    }
+    const float inv = 1.0f / (L + 1e-9f);
+    reinterpret_cast<float4*>(p.out + ((int64_t)row * p.num_heads + head) * p.head_dim)[d4] =
+        make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
 }
 
 template <int KV, int D>
 hipError_t launch_dma(const PrefillParams& p, hipStream_t stream) {
     constexpr int QT = 16 * PDims<D>::RB;
     dim3 grid((p.max_chunk_len + QT - 1) / QT, p.num_chunks,
-              p.num_kv_heads * p.head_groups);
+              p.num_kv_heads * p.head_groups * max(p.splits, 1));
     size_t lds = prefill_lds_bytes(KV, D, p.max_blocks);
 #ifdef VCPP_PREFILL_LDS_PAD
     lds = std::max<size_t>(lds, VCPP_PREFILL_LDS_PAD);
@@ -99,8 +132,20 @@ hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream) {
     }
 #undef VCPP_PF_D
     if (err != hipSuccess) return err;
+    if (p.splits > 1) {
+        const int64_t threads = (int64_t)p.rows_cap * p.num_heads * (p.head_dim / 4);
+        hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, p);
+        err = hipGetLastError();
+        if (err != hipSuccess) return err;
+    }
     if (prof) prof_end(kKernelPrefill, stream);
     return hipSuccess;
+}
+
+size_t prefill_split_bytes(int splits, int rows_cap, int num_heads, int head_dim) {
+    if (splits <= 1) return 0;
+    const size_t rows = (size_t)splits * rows_cap * num_heads;
+    return ((rows * head_dim * sizeof(float) + 255) & ~size_t(255)) + rows * sizeof(float2);
 }
 
 }  // namespace vcpp

@@ -176,10 +176,12 @@ __device__ __forceinline__ float max_over_groups(float x) {
 }
 
 // One workgroup's work: query tile bx (0 = the chunk's last, heaviest tile)
-// of chunk by, kv head / head group bz; lds is the workgroup's dynamic LDS
-// (prefill_lds_bytes).  Returns with every DMA it issued complete.
+// of chunk by, kv head / head group bz, key part `part` of p.splits; lds is
+// the workgroup's dynamic LDS (prefill_lds_bytes).  Returns with every DMA it
+// issued complete.
 template <int KV, int D, bool F>
-__device__ __forceinline__ void prefill_tile(const PrefillParams& p, int bx, int by, int bz, lds_char* lds) {
+__device__ __forceinline__ void prefill_tile(const PrefillParams& p, int bx, int by, int bz, int part,
+                                             lds_char* lds) {
     using DD = DmaDims<D, F>;
     constexpr bool BYTES = KV != VCPP_KV_F16;  // int8 / FP8: byte ring widened to fp16
     constexpr bool SCALED = KV == VCPP_KV_I8;  // per-key fp16 scales
@@ -217,6 +219,11 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int bx, int
     const int kv_end = prefix + min(t0 + kQTile, n);
     const int nblk = (kv_end + kKBlk - 1) / kKBlk;
     const int nfree = (prefix + t0 + 1) / kKBlk;  // blocks visible to every row
+    // This part's key blocks [kb_lo, kb_hi): whole block pairs, the last part
+    // up to nblk.
+    const int npairs = (nblk + 1) / 2;
+    const int kb_lo = 2 * (int)((int64_t)part * npairs / p.splits);
+    const int kb_hi = min(2 * (int)((int64_t)(part + 1) * npairs / p.splits), nblk);
 
     // Q fragments (B operand of S^T = K Q^T).
     h8 qa[RB][NC32 > 0 ? NC32 : 1];
@@ -552,10 +559,10 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int bx, int
     static_assert(kStages >= 4 && kStages % 2 == 0, "ring holds whole pairs");
     if constexpr (BYTES) {
 #pragma unroll
-        for (int s = 0; s < kStages - 2; ++s) issue8(s);
+        for (int s = 0; s < kStages - 2; ++s) issue8(kb_lo + s);
     } else {
 #pragma unroll
-        for (int s = 0; s < kStages - 2; ++s) issue(s);
+        for (int s = 0; s < kStages - 2; ++s) issue(kb_lo + s);
     }
     const int free_end = any_bad ? 0 : (min(nfree, nblk) & ~1);
     auto step = [&](int kb) {
@@ -578,12 +585,12 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int bx, int
     };
     // Two loops, one inlined compute each (one loop with both variants
     // merges their accumulators and spills).
-    for (int kb = 0; kb < free_end; kb += 2) {
+    for (int kb = kb_lo; kb < min(free_end, kb_hi); kb += 2) {
         step(kb);
 #pragma unroll 1
         for (int h = 0; h < 2; ++h) compute(kb + h, std::false_type{});
     }
-    for (int kb = free_end; kb < nblk; kb += 2) {
+    for (int kb = max(free_end, kb_lo); kb < kb_hi; kb += 2) {
         step(kb);
 #pragma unroll 1
         for (int h = 0; h < 2; ++h) compute(kb + h, std::true_type{});
@@ -591,6 +598,27 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int bx, int
     wait_vmcnt<0>();
 
     if (!head_ok) return;  // (no barrier follows)
+    if (p.splits > 1) {
+        // Part outputs: o unnormalised, (m, l) of each row from lanes g == 0.
+        const int64_t pbase = (int64_t)part * p.rows_cap;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const float rowsum = sum_over_groups(lsum[rb]);  // row c
+            const int tc = t0 + 16 * rb + c;
+            if (g == 0 && tc < n)
+                p.ws_ml[(pbase + q0 + tc) * p.num_heads + head] = make_float2(m_run[rb], rowsum);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tok = t0 + 16 * rb + 4 * g + r;
+                if (tok < n) {
+                    float* orow = p.ws_o + ((pbase + q0 + tok) * p.num_heads + head) * D;
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) orow[16 * t + c] = o[rb][t][r];
+                }
+            }
+        }
+        return;
+    }
     // Lane (g, c) holds rows 4 g + r, column 16 t + c.  Column pairs: for the
     // row pair (2 k, 2 k + 1) even lanes store row 2 k and odd lanes row 2 k + 1,
     // each the pair (c & ~1, + 1), the other value one DPP swap away.

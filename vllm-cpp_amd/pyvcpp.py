@@ -107,6 +107,11 @@ def open_library(path):
     L.vcpp_paged_prefill.argtypes = [ctypes.POINTER(KVPages), vp, vp, vp, i32, vp, vp, i32, i32,
                                      i32, vp]
     L.vcpp_paged_prefill.restype = ctypes.c_int
+    L.vcpp_paged_prefill_split.argtypes = [ctypes.POINTER(KVPages), vp, vp, vp, i32, vp, vp, i32, i32, i32,
+                                           i32, vp, sz, vp]
+    L.vcpp_paged_prefill_split.restype = ctypes.c_int
+    L.vcpp_prefill_workspace_size.argtypes = [ctypes.POINTER(KVPages), i32, i32, i32, i32]
+    L.vcpp_prefill_workspace_size.restype = sz
     L.vcpp_paged_mixed_step.argtypes = [ctypes.POINTER(KVPages), vp, vp, vp, i32, vp, vp, i32, i32,
                                         vp, vp, vp, i32, vp, vp, i32, i32, i32, vp, sz, vp]
     L.vcpp_paged_mixed_step.restype = ctypes.c_int
@@ -254,6 +259,28 @@ def paged_mixed_step(pages, dq, dout, d_tables, context_lens, max_context_len, p
                                      _ptr(prefix_lens), num_chunks, max_chunk_len, num_heads,
                                      _ptr(workspace), ws_bytes, _stream(stream))
     _check(rc)
+
+
+def prefill_workspace_size(pages, num_chunks, max_chunk_len, max_prefix_len, num_heads):
+    return lib().vcpp_prefill_workspace_size(ctypes.byref(pages), num_chunks, max_chunk_len, max_prefix_len,
+                                             num_heads)
+
+
+def paged_prefill_split(pages, q, out, block_tables, q_start, prefix_lens, max_chunk_len, max_prefix_len,
+                        num_heads, workspace=None, stream=None):
+    """vcpp_paged_prefill_split on device tensors (q fp16, out fp32)."""
+    nc = prefix_lens.shape[0]
+    need = prefill_workspace_size(pages, nc, max_chunk_len, max_prefix_len, num_heads)
+    if workspace is None and need > 0:
+        import torch
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_bytes = workspace.numel() if workspace is not None else 0
+    rc = lib().vcpp_paged_prefill_split(ctypes.byref(pages), _ptr(q), _ptr(out), _ptr(block_tables),
+                                        block_tables.shape[1], _ptr(q_start), _ptr(prefix_lens), nc,
+                                        max_chunk_len, max_prefix_len, num_heads, _ptr(workspace), ws_bytes,
+                                        _stream(stream))
+    _check(rc)
+    return out
 
 
 def write_kv(pages, k, v, slots, fp16_round_nearest=False, stream=None):
