@@ -239,7 +239,7 @@ void test_attention(KVDtype dt) {
     // Reserve a few blocks so tables are not the identity.
     std::vector<int32_t> junk;
     CHECK(m.alloc_blocks(7, junk), "alloc");
-    const int32_t lens[4] = {1, 300, 17, 777};
+    const int32_t lens[4] = {1, 300, 17, 1777};
     std::vector<std::vector<int32_t>> tables(4);
     std::vector<std::vector<float>> ks, vs;
     for (int r = 0; r < 4; ++r) {
@@ -317,8 +317,9 @@ void test_attention(KVDtype dt) {
     }
     std::printf("ok   %-58s\n", "read_kv_prefill");
     // 6. paged_prefill: the last 200 tokens of request 3 as one chunk on its
-    // 577-token prefix, host fp32 q and out (the engine's prefill buffers);
-    // row i is the reference's per-position attention over 0 .. 577 + i.
+    // 1577-token prefix (few workgroups on a long prefix: the keys of each
+    // tile are split), host fp32 q and out (the engine's prefill buffers);
+    // row i is the reference's per-position attention over 0 .. 1577 + i.
     {
         const int32_t n = 200, pre = lens[3] - n;
         std::vector<float> qc = normal(400, (size_t)n * H * D), wc((size_t)n * H * D), gc((size_t)n * H * D, NAN);

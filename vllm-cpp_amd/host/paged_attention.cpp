@@ -326,10 +326,12 @@ void paged_prefill_batch(const std::vector<PrefillChunk>& chunks, const BlockPoo
                  "paged_prefill (fp32 pages)");
     } else {
         std::vector<int32_t> tables((size_t)C * max_blocks, -1), meta(2 * (size_t)C + 1);
+        int32_t max_prefix = 0;
         for (int32_t j = 0; j < C; ++j) {
             const PrefillChunk& c = chunks[live[j]];
             std::copy(c.block_table->begin(), c.block_table->end(), tables.begin() + (size_t)j * max_blocks);
             meta[C + 1 + j] = c.prefix_len;
+            max_prefix = std::max(max_prefix, c.prefix_len);
         }
         for (int32_t j = 0; j <= C; ++j) meta[j] = rows0[j];
         uint16_t* q16 = static_cast<uint16_t*>(st.k.get(row * R * sizeof(uint16_t), s));
@@ -343,7 +345,12 @@ void paged_prefill_batch(const std::vector<PrefillChunk>& chunks, const BlockPoo
         hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, qd,
                            reinterpret_cast<_Float16*>(q16), nq);
         check(hipGetLastError(), "prefill q to fp16");
-        check_rc(vcpp_paged_prefill(&pages, q16, od, td, max_blocks, md, md + C + 1, C, max_len, num_heads, s),
+        // Few chunks on long prefixes split each tile's keys over several
+        // workgroups (the size is 0 when the chunks fill the GPU already).
+        const size_t wsb = vcpp_prefill_workspace_size(&pages, C, max_len, max_prefix, num_heads);
+        void* ws = wsb ? st.ws.get(wsb, s) : nullptr;
+        check_rc(vcpp_paged_prefill_split(&pages, q16, od, td, max_blocks, md, md + C + 1, C, max_len, max_prefix,
+                                          num_heads, ws, wsb, s),
                  "paged_prefill");
     }
     for (int32_t j = 0; j < C; ++j) {
