@@ -316,12 +316,12 @@ void test_attention(KVDtype dt) {
         }
     }
     std::printf("ok   %-58s\n", "read_kv_prefill");
-    // 6. paged_prefill: the last 200 tokens of request 3 as one chunk on its
-    // 1577-token prefix (few workgroups on a long prefix: the keys of each
+    // 6. paged_prefill: the last 100 tokens of request 3 as one chunk on its
+    // 1677-token prefix (few workgroups on a long prefix: the keys of each
     // tile are split), host fp32 q and out (the engine's prefill buffers);
-    // row i is the reference's per-position attention over 0 .. 1577 + i.
+    // row i is the reference's per-position attention over 0 .. 1677 + i.
     {
-        const int32_t n = 200, pre = lens[3] - n;
+        const int32_t n = 100, pre = lens[3] - n;
         std::vector<float> qc = normal(400, (size_t)n * H * D), wc((size_t)n * H * D), gc((size_t)n * H * D, NAN);
         for (int32_t i = 0; i < n; ++i)
             orc_paged_attention(&op, qc.data() + (size_t)i * H * D, tables[3].data(), (int32_t)tables[3].size(),

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
-from gpu_util import DevPool, assert_close, gpu_decode, gpu_prefill, prefill_tables
+from gpu_util import DevPool, assert_close, gpu_decode, gpu_prefill, gpu_prefill_split, prefill_tables
 
 pytestmark = pytest.mark.gpu
 
@@ -81,3 +81,30 @@ def test_prefill_random(cuda, case):
     want = O.prefill(pool, q16.astype(np.float32), tables, q_start, prefix, H)
     got = gpu_prefill(DevPool(pool), q16.view(np.uint16), tables, q_start, prefix, H)
     assert_close(got, want, *TOL[kind], what="prefill case %d" % case)
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_prefill_split_random(cuda, case):
+    """vcpp_paged_prefill_split on few chunks with long, ragged prefixes (the
+    shapes it splits) and some it leaves unsplit."""
+    rng = np.random.default_rng(8500 + case)
+    kind = int(rng.choice([O.ORC_F16, O.ORC_I8, O.ORC_FP8]))
+    H, Hkv = HEADS[int(rng.integers(len(HEADS)))]
+    D = int(rng.choice([64, 80, 128]))
+    nc = int(rng.integers(1, 4))
+    prefix = rng.integers(0, 5000, nc).astype(np.int32)
+    prefix[rng.random(nc) < 0.2] = 0
+    chunk = rng.integers(0, 200, nc).astype(np.int32)
+    chunk[0] = max(int(chunk[0]), 1)
+    lens = [int(p + c) for p, c in zip(prefix, chunk)]
+    nb = sum((l + 15) // 16 for l in lens) + 4
+    print("split prefill case %d: kind %d H %d Hkv %d D %d chunks %s prefixes %s"
+          % (case, kind, H, Hkv, D, list(chunk), list(prefix)), flush=True)
+    pool = O.make_pool(kind, 8600 + case, nb, Hkv, D)
+    q_start = np.concatenate([[0], np.cumsum(chunk)]).astype(np.int32)
+    q16 = O.normal(8700 + case, (int(q_start[-1]), H, D)).astype(np.float16)
+    tables = prefill_tables(8800 + case, lens, nb)
+    want = O.prefill(pool, q16.astype(np.float32), tables, q_start, prefix, H)
+    got, split = gpu_prefill_split(DevPool(pool), q16.view(np.uint16), tables, q_start, prefix, H)
+    print("  split: %s" % split, flush=True)
+    assert_close(got, want, *TOL[kind], what="split prefill case %d" % case)

@@ -572,7 +572,7 @@ static int32_t prefill_splits(const vcpp_kv_pages* kv, int32_t num_chunks, int32
     if (items >= slots) return 1;
     const int64_t want = (slots + items - 1) / items;
     const int64_t by_len = ((int64_t)max_prefix_len + max_chunk_len) / (16 * 32);
-    return (int32_t)std::max<int64_t>(1, std::min<int64_t>({want, by_len, 16}));
+    return (int32_t)std::max<int64_t>(1, std::min<int64_t>({want, by_len, (int64_t)vcpp::kMaxPrefillSplits}));
 }
 
 size_t vcpp_prefill_workspace_size(const vcpp_kv_pages* kv, int32_t num_chunks, int32_t max_chunk_len,

@@ -51,6 +51,8 @@ struct PrefillParams {
 
 hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream);
 // Workspace bytes of a split prefill (0 when splits <= 1).
+// Most key parts a split prefill cuts a query tile into.
+constexpr int kMaxPrefillSplits = 16;
 size_t prefill_split_bytes(int splits, int rows_cap, int num_heads, int head_dim);
 int prefill_head_groups(int group);
 // Dynamic LDS bytes of the prefill kernel for a table of max_blocks entries.

@@ -41,21 +41,32 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
     if (row >= p.q_start[p.num_chunks]) return;
     const int rem = (int)(idx - row * per_row);
     const int head = rem / D4, d4 = rem - head * D4;
+    // One pass, all parts' loads issued together; parts with an empty key
+    // range (sum 0) weigh 0.
+    float2 ml[kMaxPrefillSplits];
+    float4 v[kMaxPrefillSplits];
     float M = -__builtin_inff();
-    for (int s = 0; s < p.splits; ++s)
-        M = fmaxf(M, p.ws_ml[((int64_t)s * p.rows_cap + row) * p.num_heads + head].x);
+#pragma unroll
+    for (int s = 0; s < kMaxPrefillSplits; ++s) {
+        if (s < p.splits) {
+            const int64_t rh = ((int64_t)s * p.rows_cap + row) * p.num_heads + head;
+            ml[s] = p.ws_ml[rh];
+            v[s] = reinterpret_cast<const float4*>(p.ws_o + rh * p.head_dim)[d4];
+            if (ml[s].y > 0.f) M = fmaxf(M, ml[s].x);
+        }
+    }
     float L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s = 0; s < p.splits; ++s) {
-        const int64_t rh = ((int64_t)s * p.rows_cap + row) * p.num_heads + head;
-        const float2 ml = p.ws_ml[rh];
-        const float w = ml.y > 0.f ? exp2f(ml.x - M) : 0.f;  // empty parts weigh 0
-        L += w * ml.y;
-        const float4 v = reinterpret_cast<const float4*>(p.ws_o + rh * p.head_dim)[d4];
-        acc.x += w * v.x;
-        acc.y += w * v.y;
-        acc.z += w * v.z;
-        acc.w += w * v.w;
+#pragma unroll
+    for (int s = 0; s < kMaxPrefillSplits; ++s) {
+        if (s < p.splits && ml[s].y > 0.f) {
+            const float w = exp2f(ml[s].x - M);
+            L += w * ml[s].y;
+            acc.x += w * v[s].x;
+            acc.y += w * v[s].y;
+            acc.z += w * v[s].z;
+            acc.w += w * v[s].w;
+        }
     }
     const float inv = 1.0f / (L + 1e-9f);
     reinterpret_cast<float4*>(p.out + ((int64_t)row * p.num_heads + head) * p.head_dim)[d4] =
