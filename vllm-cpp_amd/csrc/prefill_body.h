@@ -605,12 +605,14 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int bx, int
         for (int rb = 0; rb < RB; ++rb) {
             const float rowsum = sum_over_groups(lsum[rb]);  // row c
             const int tc = t0 + 16 * rb + c;
-            if (g == 0 && tc < n)
+            // (rows past rows_cap -- chunks longer than max_chunk_len, a
+            // caller error -- are not stored; their output stays unwritten)
+            if (g == 0 && tc < n && q0 + tc < p.rows_cap)
                 p.ws_ml[(pbase + q0 + tc) * p.num_heads + head] = make_float2(m_run[rb], rowsum);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int tok = t0 + 16 * rb + 4 * g + r;
-                if (tok < n) {
+                if (tok < n && q0 + tok < p.rows_cap) {
                     float* orow = p.ws_o + ((pbase + q0 + tok) * p.num_heads + head) * D;
 #pragma unroll
                     for (int t = 0; t < NT; ++t) orow[16 * t + c] = o[rb][t][r];
