@@ -490,6 +490,7 @@ vcpp::PrefillParams prefill_params(const vcpp_kv_pages* kv, const uint16_t* q, f
     p.scale_log2 = (1.0f / std::sqrt((float)kv->head_dim)) * 1.4426950408889634f;
     p.bs_magic = ((1ull << 40) + kv->block_size - 1) / kv->block_size;
     p.splits = 1;
+    p.xcd_cus = device_cus() / 8;
     p.rows_cap = (int32_t)std::min<int64_t>((int64_t)num_chunks * max_chunk_len, INT32_MAX);
 #ifdef VCPP_GATHER_DUMP
     p.gather_dump = g_gather_dump;

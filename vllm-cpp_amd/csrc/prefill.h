@@ -43,6 +43,7 @@ struct PrefillParams {
     float* ws_o;       // [splits][rows_cap][num_heads][head_dim]
     float2* ws_ml;     // [splits][rows_cap][num_heads] (max in log2 units, sum)
     uint64_t bs_magic; // ceil(2^40 / block_size): pos / block_size = (pos * bs_magic) >> 40
+    int32_t xcd_cus;   // CUs per XCD (0: unknown; no pairing of heavy and light tiles)
 #ifdef VCPP_GATHER_DUMP
     int32_t* gather_dump;    // checker builds: [rows][gather_stride][2] (block, slot)
     int64_t gather_stride;

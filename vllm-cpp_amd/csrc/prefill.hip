@@ -20,7 +20,19 @@ void prefill_dma_kernel(PrefillParams p) {
     const int total = nx * ny * gridDim.z;
     if ((total & 7) == 0) {
         const int lin = bx + nx * (by + ny * bz);
-        const int m = (lin & 7) * (total >> 3) + (lin >> 3);
+        const int per = total >> 3;  // ids per XCD
+        int j = lin >> 3;            // dispatch order within the XCD
+#ifndef VCPP_PF_NO_PAIRING
+        // A grid that fits the GPU in one round (at most two workgroups per
+        // CU): the dispatcher gives each CU of an XCD one workgroup before it
+        // gives any a second, so local ids j and j + C (C CUs per XCD) share
+        // a CU.  Reversing the order of the second ones puts the k-th
+        // heaviest tile beside the k-th lightest of the XCD's share.
+        // (Grids of several rounds keep heaviest-first order.)
+        const int C = p.xcd_cus;
+        if (C > 0 && per > C && per <= 2 * C && j >= C) j = per + C - 1 - j;
+#endif
+        const int m = (lin & 7) * per + j;
         bx = m % nx;
         by = (m / nx) % ny;
         bz = m / (nx * ny);
