@@ -189,7 +189,7 @@ int vcpp_paged_prefill(const vcpp_kv_pages* kv, const uint16_t* q, float* out,
  * vcpp_paged_prefill, plus
  *   max_prefix_len  host-side upper bound of prefix_lens (sizes the split)
  *   workspace       device scratch of at least vcpp_prefill_workspace_size(...)
- *                   bytes (none needed when that is 0)
+ *                   bytes, 16-byte aligned (none needed when that is 0)
  * Calls on one stream may share a workspace; calls that overlap may not.
  * No reference counterpart: the reference prefills one position at a time
  * (src/paged_engine.cpp:381-384).
