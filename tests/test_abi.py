@@ -159,3 +159,30 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(pyvcpp, "LIB_PATH", str(tmp_path / "absent" / "libvcpp_attn.so"))
     with pytest.raises(RuntimeError, match="not built"):
         pyvcpp.lib()
+
+
+@pytest.mark.parametrize("shape,hkv,heads,want", [
+    # (chunks, max_chunk_len, max_prefix_len): one 512-token chunk on a 32 k
+    # prefix: 8 tiles x 8 kv heads x 2 head groups = 128 workgroups -> 4 parts
+    ((1, 512, 32768), 8, 64, 4 * 512 * 64 * 80 * 4 + 4 * 512 * 64 * 8),
+    ((8, 2048, 1024), 8, 64, 0),       # config 3: 4096 workgroups fill the GPU
+    ((1, 512, 0), 8, 64, 0),           # keys too short to split (512 + 0 keys: one part)
+    ((1, 16, 6000), 1, 8, 11 * 16 * 8 * 80 * 4 + 11 * 16 * 8 * 8),  # (6000 + 16) / 512 = 11 parts
+    ((1, 64, 100000), 1, 8, 16 * 64 * 8 * 80 * 4 + 16 * 64 * 8 * 8),  # at most 16 parts
+])
+def test_prefill_split_workspace_size(shape, hkv, heads, want):
+    """The split prefill's part count and workspace ([parts][rows][heads]
+    fp32 rows of head_dim, 256-byte aligned, then (max, sum) pairs) for a
+    256-CU device (the count the library assumes without a device)."""
+    L = pyvcpp.lib()
+    pg = pages(hkv=hkv)
+    assert L.vcpp_prefill_workspace_size(ctypes.byref(pg), *shape, heads) == want
+
+
+def test_prefill_split_requires_workspace():
+    L = pyvcpp.lib()
+    pg = pages()
+    rc = L.vcpp_paged_prefill_split(ctypes.byref(pg), 4096, 4096, 4096, 2048, 4096, 4096, 1, 512, 32768, 64,
+                                    None, 0, None)
+    assert rc == pyvcpp.VCPP_E_WORKSPACE
+    assert "workspace" in pyvcpp.last_error()
