@@ -336,31 +336,31 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int bx, int
             }
         }
     };
-    // Blocks kb, kb + 1 (byte ring) -> the fp16 area.  FP8: the values.
-    // int8: K as exact fp16 integers, its per-key scale times log2(e)/sqrt(D)
-    // converted in place to fp32 for the exp's fma (at least FLT_MIN, so a
-    // masked key's -inf never meets a zero scale); V times its key's scale,
-    // one IEEE fp16 rounding of the exact product (v_pk_mul_f16).
+    // Block kb (byte ring) -> fp16 block kb & 1 of the fp16 area.  FP8: the
+    // values.  int8: K as exact fp16 integers, its per-key scale times
+    // log2(e)/sqrt(D) converted in place to fp32 for the exp's fma (at least
+    // FLT_MIN, so a masked key's -inf never meets a zero scale); V times its
+    // key's scale, one IEEE fp16 rounding of the exact product
+    // (v_pk_mul_f16).
     auto widen = [&](int kb) {
+        lds_char* st = lds + (kb % kStages) * RSTAGE;
         if constexpr (SCALED) {
-            if (tid < 64) {
-                lds_char* sw = lds + ((kb + (tid >> 5)) % kStages) * RSTAGE + ID::SCALES + (tid & 31) * 4;
+            if (tid < 32) {
+                lds_char* sw = st + ID::SCALES + tid * 4;
                 const float ks = (float)__builtin_bit_cast(
                     _Float16, *reinterpret_cast<__attribute__((address_space(3))) const uint16_t*>(sw));
                 *reinterpret_cast<__attribute__((address_space(3))) float*>(sw) =
                     fmaxf(ks * p.scale_log2, 1.17549435e-38f);
             }
         }
+        lds_char* dst0 = lds + AREA + (kb & 1) * DD::STAGE;
 #pragma unroll
-        for (int u0 = 0; u0 < 2 * ID::UNITS; u0 += 256) {
-            const int u = u0 + tid;
-            if (u < 2 * ID::UNITS) {
-                const int blk = u >= ID::UNITS;
-                const int v = u - blk * ID::UNITS;
+        for (int u0 = 0; u0 < ID::UNITS; u0 += 256) {
+            const int v = u0 + tid;
+            if (v < ID::UNITS) {
                 const int which = v >= ID::REGION;
                 const int q = v - which * ID::REGION;
                 const int ch = q >> 5, key = q & 31;
-                lds_char* st = lds + ((kb + blk) % kStages) * RSTAGE;
                 const i4 raw = *reinterpret_cast<__attribute__((address_space(3))) i4*>(st + v * 16);
                 h8 lo = bytes8_to_h8<KV>((uint32_t)raw.x, (uint32_t)raw.y);
                 h8 hi = bytes8_to_h8<KV>((uint32_t)raw.z, (uint32_t)raw.w);
@@ -372,7 +372,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int bx, int
                         hi *= sc;
                     }
                 }
-                lds_char* dst = lds + AREA + blk * DD::STAGE + which * DD::REGION * 16;
+                lds_char* dst = dst0 + which * DD::REGION * 16;
                 *reinterpret_cast<__attribute__((address_space(3))) h8*>(dst + slot_of(2 * ch, key) * 16) = lo;
                 *reinterpret_cast<__attribute__((address_space(3))) h8*>(dst + slot_of(2 * ch + 1, key) * 16) = hi;
             }
@@ -551,49 +551,63 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int bx, int
         }
     };
 
-    // Ring of kStages 32-key blocks, consumed two per barrier: while blocks
-    // kb, kb + 1 are computed, blocks up to kb + kStages - 1 are in flight.
-    // Blocks past nblk are issued too (as zero chunks) so that every wave's
-    // vmcnt arithmetic below stays exact, and an odd tail block is paired
-    // with a fully masked one.
+    // fp16 pages: a ring of kStages 32-key blocks, consumed two per barrier:
+    // while blocks kb, kb + 1 are computed, blocks up to kb + kStages - 1 are
+    // in flight.  Byte pages: a ring of kStages byte blocks and two fp16
+    // blocks, one block per barrier: block kb is computed from its fp16 copy
+    // while block kb + 1 is widened into the other one and blocks up to
+    // kb + kStages - 2 are in flight.  Blocks past nblk are issued too (as
+    // zero chunks) so that every wave's vmcnt arithmetic below stays exact;
+    // on fp16 pages an odd tail block is paired with a fully masked one.
     static_assert(kStages >= 4 && kStages % 2 == 0, "ring holds whole pairs");
+    const int free_end = any_bad ? 0 : (min(nfree, nblk) & ~1);
     if constexpr (BYTES) {
 #pragma unroll
-        for (int s = 0; s < kStages - 2; ++s) issue8(kb_lo + s);
+        for (int s = 0; s < kStages - 1; ++s) issue8(kb_lo + s);
+        if (my_inst8 == PERW8) wait_vmcnt<(kStages - 2) * PERW8>();
+        else wait_vmcnt<(kStages - 2) * (PERW8 - 1)>();
+        __syncthreads();  // block kb_lo landed for every wave
+        if (kb_lo < kb_hi) widen(kb_lo);
+        auto step8 = [&](int kb) {
+            if (my_inst8 == PERW8) wait_vmcnt<(kStages - 3) * PERW8>();
+            else wait_vmcnt<(kStages - 3) * (PERW8 - 1)>();
+            // Block kb + 1 landed for every wave, block kb widened, block
+            // kb - 1 computed (its byte stage and fp16 block are free).
+            __syncthreads();
+            issue8(kb + kStages - 1);
+            if (kb + 1 < kb_hi) widen(kb + 1);
+        };
+        for (int kb = kb_lo; kb < min(free_end, kb_hi); ++kb) {
+            step8(kb);
+            compute(kb, std::false_type{});
+        }
+        for (int kb = max(free_end, kb_lo); kb < kb_hi; ++kb) {
+            step8(kb);
+            compute(kb, std::true_type{});
+        }
     } else {
 #pragma unroll
         for (int s = 0; s < kStages - 2; ++s) issue(kb_lo + s);
-    }
-    const int free_end = any_bad ? 0 : (min(nfree, nblk) & ~1);
-    auto step = [&](int kb) {
-        constexpr int kAhead = kStages - 4;  // blocks allowed in flight at the wait
-        if constexpr (BYTES) {
-            if (my_inst8 == PERW8) wait_vmcnt<kAhead * PERW8>();
-            else wait_vmcnt<kAhead * (PERW8 - 1)>();
-            __syncthreads();  // blocks kb, kb + 1 landed; the fp16 area is free again
-            issue8(kb + kStages - 2);
-            issue8(kb + kStages - 1);
-            widen(kb);
-            __syncthreads();  // fp16 area holds blocks kb, kb + 1
-        } else {
+        auto step = [&](int kb) {
+            constexpr int kAhead = kStages - 4;  // blocks allowed in flight at the wait
             if (my_inst == PERW) wait_vmcnt<kAhead * PERW>();
             else wait_vmcnt<kAhead * (PERW - 1)>();
             __syncthreads();  // blocks kb, kb + 1 landed for all waves; kb - 2, kb - 1 consumed
             issue(kb + kStages - 2);
             issue(kb + kStages - 1);
+        };
+        // Two loops, one inlined compute each (one loop with both variants
+        // merges their accumulators and spills).
+        for (int kb = kb_lo; kb < min(free_end, kb_hi); kb += 2) {
+            step(kb);
+#pragma unroll 1
+            for (int h = 0; h < 2; ++h) compute(kb + h, std::false_type{});
         }
-    };
-    // Two loops, one inlined compute each (one loop with both variants
-    // merges their accumulators and spills).
-    for (int kb = kb_lo; kb < min(free_end, kb_hi); kb += 2) {
-        step(kb);
+        for (int kb = max(free_end, kb_lo); kb < kb_hi; kb += 2) {
+            step(kb);
 #pragma unroll 1
-        for (int h = 0; h < 2; ++h) compute(kb + h, std::false_type{});
-    }
-    for (int kb = max(free_end, kb_lo); kb < kb_hi; kb += 2) {
-        step(kb);
-#pragma unroll 1
-        for (int h = 0; h < 2; ++h) compute(kb + h, std::true_type{});
+            for (int h = 0; h < 2; ++h) compute(kb + h, std::true_type{});
+        }
     }
     wait_vmcnt<0>();
 
