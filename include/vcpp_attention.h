@@ -211,12 +211,19 @@ size_t vcpp_prefill_workspace_size(const vcpp_kv_pages* kv, int32_t num_chunks, 
  * d_* / dq / dout / num_seqs / max_context_len, balanced split) and the
  * prefill of vcpp_paged_prefill (pq / pout / p_* / q_start / prefix_lens /
  * num_chunks / max_chunk_len) over the same pages, with the same results.
- * Where the shape allows (fp16, int8 or FP8 pages; head_dim 64 or 80;
- * num_kv_heads a multiple of 4; <= 8 query heads per kv head; a CU count that
- * is a multiple of 8) both run in ONE launch that keeps the HBM-bound decode
- * and the MFMA-bound prefill on every CU at once, followed by the decode's
- * merge; otherwise as the two calls on `stream`, decode first.  Either side
- * may be empty (num_seqs == 0, or num_chunks == 0).
+ * By default the decode kernel and then the prefill kernel run on `stream`;
+ * when both sides are present, the decode's split-K merge runs on a
+ * library-owned side stream (default priority, one per device) that waits
+ * for the decode kernel by an event, so that it overlaps the prefill, and
+ * `stream` waits for it by another event before the call returns: all
+ * results are ordered on `stream` as with the two separate calls
+ * (VCPP_NO_MERGE_FORK=1 keeps the merge on `stream`).  With
+ * VCPP_MIXED_FUSED=1, where the shape allows (fp16, int8 or FP8 pages;
+ * head_dim 64 or 80; num_kv_heads a multiple of 4; <= 8 query heads per kv
+ * head; a CU count that is a multiple of 8), both run in ONE launch that
+ * keeps the decode and the prefill on every CU at once, followed by the
+ * decode's merge (slower on MI355X; kept for measurement).  Either side may
+ * be empty (num_seqs == 0, or num_chunks == 0).
  *   workspace    device scratch of at least vcpp_mixed_workspace_size(...)
  */
 int vcpp_paged_mixed_step(const vcpp_kv_pages* kv, const float* dq, float* dout,

@@ -91,6 +91,33 @@ int device_cus() {
     return cus[dev];
 }
 
+// The mixed step's side stream (default priority) and fork / join events,
+// one set per device, made on first use and kept for the process.  Calls
+// that use them hold g_fork_mu from the fork to the join's enqueue.
+std::mutex g_fork_mu;
+
+const vcpp::MergeFork* merge_fork() {
+    static vcpp::MergeFork mf[64];
+    static int state[64] = {};  // 0 not made, 1 made, -1 failed
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    if (state[dev] == 0) {
+        bool ok = hipStreamCreateWithFlags(&mf[dev].side, hipStreamNonBlocking) == hipSuccess;
+        ok = ok && hipEventCreateWithFlags(&mf[dev].fork, hipEventDisableTiming) == hipSuccess;
+        ok = ok && hipEventCreateWithFlags(&mf[dev].join, hipEventDisableTiming) == hipSuccess;
+        state[dev] = ok ? 1 : -1;
+        if (!ok) (void)hipGetLastError();
+    }
+    return state[dev] == 1 ? &mf[dev] : nullptr;
+}
+
+// VCPP_NO_MERGE_FORK=1: the mixed step's merge stays on the caller's stream
+// (for measurement).
+bool no_merge_fork() {
+    const char* e = std::getenv("VCPP_NO_MERGE_FORK");
+    return e && e[0] == '1';
+}
+
 // Launch geometry and workspace layout of one decode call.
 struct DecodePlan {
     int32_t num_wg = 0;      // fp16/int8: workgroup ranges per kv-head group
@@ -640,6 +667,33 @@ int vcpp_paged_mixed_step(const vcpp_kv_pages* kv, const float* dq, float* dout,
     if (rc != VCPP_OK) return rc;
     const bool has_p = num_chunks > 0 && max_chunk_len > 0;
     const int32_t fg = num_seqs > 0 && has_p ? mixed_grid(kv, num_heads, p_max_blocks_per_seq) : 0;
+    if (fg == 0 && num_seqs > 0 && has_p && kv->dtype != VCPP_KV_F32 && !no_merge_fork()) {
+        // Decode, then the prefill on the caller's stream, with the decode's
+        // merge on a side stream between them (it depends on the decode
+        // only, and overlaps the prefill); the caller's stream waits for it
+        // at the end.
+        const DecodePlan pl = plan_decode(kv, num_seqs, num_heads, max_context_len, 0);
+        if (pl.max_parts > 65535) return fail(VCPP_E_UNSUPPORTED, "too many partitions (%d)", pl.max_parts);
+        rc = check_workspace(pl, workspace, workspace_bytes);
+        if (rc != VCPP_OK) return rc;
+        const vcpp::DecodeParams dp = decode_params(kv, dq, dout, d_block_tables, d_max_blocks_per_seq,
+                                                    d_table_lens, d_context_lens, num_seqs, max_context_len,
+                                                    num_heads, 0, pl, workspace);
+        const vcpp::PrefillParams pp = prefill_params(kv, pq, pout, p_block_tables, p_max_blocks_per_seq,
+                                                      q_start, prefix_lens, num_chunks, max_chunk_len, num_heads);
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        std::lock_guard<std::mutex> lock(g_fork_mu);
+        const vcpp::MergeFork* mf = merge_fork();
+        hipError_t e = vcpp::launch_decode(dp, s, mf);
+        if (e != hipSuccess) return hip_fail(e, "decode launch");
+        e = vcpp::launch_prefill(pp, s);
+        if (e != hipSuccess) return hip_fail(e, "prefill launch");
+        if (mf) {
+            e = hipStreamWaitEvent(s, mf->join, 0);
+            if (e != hipSuccess) return hip_fail(e, "merge join");
+        }
+        return VCPP_OK;
+    }
     if (fg == 0) {  // two launches on the stream: decode, then prefill
         if (num_seqs > 0) {
             rc = vcpp_paged_decode(kv, dq, dout, d_block_tables, d_max_blocks_per_seq, d_table_lens,

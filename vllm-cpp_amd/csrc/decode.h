@@ -61,7 +61,15 @@ struct DecodeParams {
 #endif
 };
 
-hipError_t launch_decode(const DecodeParams& p, hipStream_t stream);
+// Fork / join of the decode's merge onto a second stream: after the decode
+// kernel, `fork` is recorded on the launch stream and `side` waits for it;
+// the merge runs on `side`, which records `join` after it.  The caller makes
+// its stream wait for `join` before anything that reads the outputs.
+struct MergeFork {
+    hipStream_t side;
+    hipEvent_t fork, join;
+};
+hipError_t launch_decode(const DecodeParams& p, hipStream_t stream, const MergeFork* mf = nullptr);
 
 // The fused mixed step: one launch of 3 workgroups per CU (cus a multiple of
 // 8), two prefill workers and one decode worker on each CU, then the decode

@@ -1632,7 +1632,7 @@ int decode_group_count(int pairs) {
     return (pairs + wpw - 1) / wpw;
 }
 
-hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
+hipError_t launch_decode(const DecodeParams& p, hipStream_t stream, const MergeFork* mf) {
     if (p.num_seqs == 0) return hipSuccess;
     hipError_t err;
     const bool prof = prof_enabled();
@@ -1689,6 +1689,12 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
 #undef VCPP_DISPATCH_D
     if (err != hipSuccess) return err;
     if (prof) prof_end(kKernelDecode, stream);
+    if (mf) {
+        err = hipEventRecord(mf->fork, stream);
+        if (err == hipSuccess) err = hipStreamWaitEvent(mf->side, mf->fork, 0);
+        if (err != hipSuccess) return err;
+        stream = mf->side;
+    }
     if (prof) prof_begin(kKernelMerge, stream);
     dim3 mg(p.num_seqs, (p.pairs + 3) / 4);
     switch (p.head_dim) {
@@ -1698,6 +1704,7 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
     }
     err = hipGetLastError();
     if (prof) prof_end(kKernelMerge, stream);
+    if (err == hipSuccess && mf) err = hipEventRecord(mf->join, stream);
     return err;
 }
 
