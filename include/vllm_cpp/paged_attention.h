@@ -47,8 +47,10 @@ void read_kv_prefill(const BlockPool& kv_manager, const std::vector<int32_t>& bl
 // pool already (write_kv_prefill).  This is the engine's prefill loop of
 // read_kv_prefill + compute_attention per position
 // (src/paged_engine.cpp:381-384, src/paged_attention.cpp:174-201) as one
-// launch: q is rounded to fp16 for the MFMA kernel (vcpp_paged_prefill) on
-// FP16 / FP8 / INT8 pools; FP32 pools run every row as an fp32 decode query.
+// launch: q is rounded to fp16 for the MFMA kernel (vcpp_paged_prefill_split,
+// which splits each query tile's keys over several workgroups when few
+// chunks sit on long prefixes) on FP16 / FP8 / INT8 pools; FP32 pools run
+// every row as an fp32 decode query.
 void paged_prefill(const float* q, const std::vector<int32_t>& block_table, int32_t prefix_len,
                    int32_t num_tokens, const BlockPool& kv_manager, int32_t num_heads,
                    int32_t num_kv_heads, int32_t head_dim, int32_t layer, float* out);
