@@ -66,3 +66,16 @@ struct PrefillChunk {
 };
 void paged_prefill_batch(const std::vector<PrefillChunk>& chunks, const BlockPool& kv_manager,
                          int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t layer);
+
+// One engine step's attention for one layer: the decoding requests (as
+// paged_attention_batch) and the prefill chunks (as paged_prefill_batch) of a
+// ScheduleOutput (src/scheduler.h:14-23), served together as the engine's
+// step serves them (src/paged_engine.cpp:254-269), through one
+// vcpp_paged_mixed_step call: the decode kernel, its merge beside the
+// prefill kernel.  Same skip rules and results as the two calls; FP32 pools,
+// and steps with only one kind of work, run as those calls.
+void paged_attention_step(const std::vector<const float*>& q_ptrs,
+                          const std::vector<const std::vector<int32_t>*>& block_tables,
+                          const std::vector<int32_t>& seq_lens, std::vector<float*> out_ptrs,
+                          const std::vector<PrefillChunk>& chunks, const BlockPool& kv_manager,
+                          int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t layer);

@@ -351,6 +351,27 @@ void test_attention(KVDtype dt) {
               "copy");
         close(g1.data(), w1.data(), g1.size(), tol, rtol, "paged_prefill_batch chunk 0, device buffers");
         close(gc.data(), wc.data(), gc.size(), tol, rtol, "paged_prefill_batch chunk 1, device buffers");
+        // 8. one step with both kinds of work (paged_attention_step): the four
+        // decode queries (host buffers) and the two chunks (host buffers).
+        {
+            std::vector<float> gd((size_t)4 * H * D, NAN), g1s(q1.size(), NAN), gcs(qc.size(), NAN);
+            std::vector<const float*> sq;
+            std::vector<float*> so;
+            std::vector<const std::vector<int32_t>*> stb;
+            std::vector<int32_t> ssl;
+            for (int r = 0; r < 4; ++r) {
+                sq.push_back(q.data() + (size_t)r * H * D);
+                so.push_back(gd.data() + (size_t)r * H * D);
+                stb.push_back(&tables[r]);
+                ssl.push_back(lens[r]);
+            }
+            paged_attention_step(sq, stb, ssl, so,
+                                 {{q1.data(), &tables[1], 0, n1, g1s.data()}, {qc.data(), &tables[3], pre, n, gcs.data()}},
+                                 m.block_pool(), H, HKV, D, layer);
+            close(gd.data(), want.data(), gd.size(), tol, rtol, "paged_attention_step decodes, host buffers");
+            close(g1s.data(), w1.data(), g1s.size(), tol, rtol, "paged_attention_step chunk 0, host buffers");
+            close(gcs.data(), wc.data(), gcs.size(), tol, rtol, "paged_attention_step chunk 1, host buffers");
+        }
         for (float* p : {q1d, o1d, qcd, ocd}) (void)hipFree(p);
     }
     (void)hipFree(qd);

@@ -362,3 +362,112 @@ void paged_prefill_batch(const std::vector<PrefillChunk>& chunks, const BlockPoo
     }
     if (any_host) check(hipStreamSynchronize(s), "paged_prefill sync");
 }
+
+void paged_attention_step(const std::vector<const float*>& q_ptrs,
+                          const std::vector<const std::vector<int32_t>*>& block_tables,
+                          const std::vector<int32_t>& seq_lens, std::vector<float*> out_ptrs,
+                          const std::vector<PrefillChunk>& chunks, const BlockPool& kv_manager,
+                          int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t layer) {
+    if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return;
+    vcpp_kv_pages pages;
+    if (!attention_pages(kv_manager, layer, num_kv_heads, head_dim, &pages)) return;
+    // Decoding requests with a table, prefill chunks with a table and tokens
+    // (the others are skipped, as by the two calls).
+    std::vector<size_t> dl, pl;
+    int32_t dmb = 1, max_ctx = 0, pmb = 1, max_len = 0;
+    const size_t n = std::min({q_ptrs.size(), block_tables.size(), seq_lens.size(), out_ptrs.size()});
+    for (size_t i = 0; i < n; ++i) {
+        if (!block_tables[i]) continue;
+        dl.push_back(i);
+        dmb = std::max<int32_t>(dmb, (int32_t)block_tables[i]->size());
+        max_ctx = std::max(max_ctx, seq_lens[i]);
+    }
+    for (size_t i = 0; i < chunks.size(); ++i) {
+        const PrefillChunk& c = chunks[i];
+        if (!c.block_table || c.num_tokens <= 0 || c.prefix_len < 0 || !c.q || !c.out) continue;
+        pl.push_back(i);
+        pmb = std::max<int32_t>(pmb, (int32_t)c.block_table->size());
+        max_len = std::max(max_len, c.num_tokens);
+    }
+    if (pages.dtype == VCPP_KV_F32 || dl.empty() || pl.empty()) {
+        if (!dl.empty())
+            paged_attention_batch(q_ptrs, block_tables, seq_lens, kv_manager, num_heads, num_kv_heads, head_dim,
+                                  layer, out_ptrs);
+        if (!pl.empty()) paged_prefill_batch(chunks, kv_manager, num_heads, num_kv_heads, head_dim, layer);
+        return;
+    }
+    hipStream_t s = static_cast<hipStream_t>(kv_manager.stream());
+    const size_t row = (size_t)num_heads * head_dim;
+    const int32_t B = (int32_t)dl.size(), C = (int32_t)pl.size();
+    // Host-side argument blocks: decode tables then prefill tables; decode
+    // context lengths, table lengths, then the chunks' row starts and
+    // prefix lengths.
+    std::vector<int32_t> tables((size_t)B * dmb + (size_t)C * pmb, -1), meta(2 * (size_t)B + 2 * C + 1);
+    for (int32_t b = 0; b < B; ++b) {
+        const auto& t = *block_tables[dl[b]];
+        std::copy(t.begin(), t.end(), tables.begin() + (size_t)b * dmb);
+        meta[b] = std::max(seq_lens[dl[b]], 0);
+        meta[B + b] = (int32_t)t.size();
+    }
+    std::vector<int32_t> rows0{0};
+    for (int32_t j = 0; j < C; ++j) {
+        const PrefillChunk& c = chunks[pl[j]];
+        std::copy(c.block_table->begin(), c.block_table->end(), tables.begin() + (size_t)B * dmb + (size_t)j * pmb);
+        rows0.push_back(rows0.back() + c.num_tokens);
+        meta[2 * B + C + 1 + j] = c.prefix_len;
+    }
+    for (int32_t j = 0; j <= C; ++j) meta[2 * B + j] = rows0[j];
+    const int32_t R = rows0.back();
+
+    PoolStaging& st = kv_manager.staging();
+    std::lock_guard<std::mutex> lock(st.mu);
+    float* qd = static_cast<float*>(st.q.get(row * ((size_t)B + R) * sizeof(float), s));
+    float* od = static_cast<float*>(st.out.get(row * ((size_t)B + R) * sizeof(float), s));
+    uint16_t* q16 = static_cast<uint16_t*>(st.k.get(row * R * sizeof(uint16_t), s));
+    int32_t* td = static_cast<int32_t*>(st.tables.get(tables.size() * sizeof(int32_t), s));
+    int32_t* md = static_cast<int32_t*>(st.ctx.get(meta.size() * sizeof(int32_t), s));
+    float* qp = qd + row * B;
+    float* op = od + row * B;
+    bool any_host = false;
+    for (int32_t b = 0; b < B; ++b) {
+        const float* src = q_ptrs[dl[b]];
+        const bool dev = is_device(src);
+        any_host |= !dev;
+        check(hipMemcpyAsync(qd + row * b, src, row * sizeof(float),
+                             dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, s), "step decode q");
+    }
+    for (int32_t j = 0; j < C; ++j) {
+        const PrefillChunk& c = chunks[pl[j]];
+        const bool dev = is_device(c.q);
+        any_host |= !dev;
+        check(hipMemcpyAsync(qp + row * rows0[j], c.q, row * c.num_tokens * sizeof(float),
+                             dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, s), "step prefill q");
+    }
+    check(hipMemcpyAsync(td, tables.data(), tables.size() * sizeof(int32_t), hipMemcpyHostToDevice, s),
+          "step tables");
+    check(hipMemcpyAsync(md, meta.data(), meta.size() * sizeof(int32_t), hipMemcpyHostToDevice, s), "step lens");
+    const int64_t nq = (int64_t)row * R;
+    hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, qp,
+                       reinterpret_cast<_Float16*>(q16), nq);
+    check(hipGetLastError(), "step q to fp16");
+    const size_t wsb = vcpp_mixed_workspace_size(&pages, B, num_heads, max_ctx, pmb);
+    void* ws = wsb ? st.ws.get(wsb, s) : nullptr;
+    check_rc(vcpp_paged_mixed_step(&pages, qd, od, td, dmb, md + B, md, B, max_ctx, q16, op, td + (size_t)B * dmb,
+                                   pmb, md + 2 * B, md + 2 * B + C + 1, C, max_len, num_heads, ws, wsb, s),
+             "paged_attention_step");
+    for (int32_t b = 0; b < B; ++b) {
+        float* dst = out_ptrs[dl[b]];
+        const bool dev = is_device(dst);
+        any_host |= !dev;
+        check(hipMemcpyAsync(dst, od + row * b, row * sizeof(float),
+                             dev ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, s), "step decode out");
+    }
+    for (int32_t j = 0; j < C; ++j) {
+        const PrefillChunk& c = chunks[pl[j]];
+        const bool dev = is_device(c.out);
+        any_host |= !dev;
+        check(hipMemcpyAsync(c.out, op + row * rows0[j], row * c.num_tokens * sizeof(float),
+                             dev ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, s), "step prefill out");
+    }
+    if (any_host) check(hipStreamSynchronize(s), "paged_attention_step sync");
+}
