@@ -1416,19 +1416,24 @@ __device__ __forceinline__ void decode_page_body(const DecodeParams& p, int bx, 
             int carry = 0;
             for (int base = 0; base < p.num_seqs; base += 64) {
                 const int sl = base + lane;
-                const int nt = sl < p.num_seqs ? tiles_of(p, sl) : 0;
+                // This lane's sequence: its context length (tiles) and table
+                // length, loaded together; the sequences the window overlaps
+                // read them by lane below instead of with loads of their own.
+                const bool in = sl < p.num_seqs;
+                const int ctx_l = in ? min(max(p.context_lens[sl], 0), p.ctx_cap) : 0;
+                const int tlen_l = in && p.table_lens ? min(p.max_blocks, p.table_lens[sl]) : p.max_blocks;
+                const int nt = (ctx_l + kTile - 1) / kTile;
                 const int Sl = carry + wave_excl_scan(nt, lane);
                 carry += wave_sum(nt);
-                uint64_t todo = __ballot(sl < p.num_seqs && nt > 0 && Sl < win1 && Sl + nt > win0);
+                uint64_t todo = __ballot(in && nt > 0 && Sl < win1 && Sl + nt > win0);
                 while (todo) {
                     const int j = __builtin_ctzll(todo);
                     todo &= todo - 1;
                     const int s = base + j;
                     const int S = __builtin_amdgcn_readlane(Sl, j);
                     const int n = __builtin_amdgcn_readlane(nt, j);
-                    const int ctx = min(max(p.context_lens[s], 0), p.ctx_cap);
-                    int tlen = p.max_blocks;
-                    if (p.table_lens) tlen = min(tlen, p.table_lens[s]);
+                    const int ctx = __builtin_amdgcn_readlane(ctx_l, j);
+                    const int tlen = __builtin_amdgcn_readlane(tlen_l, j);
                     const int end = (int)min((int64_t)ctx, (int64_t)tlen * p.block_size);
                     const int t0 = max(win0, S), t1 = min(win1, S + n);
                     if constexpr (PRE_Q) {
