@@ -44,7 +44,10 @@ void prefill_dma_kernel(PrefillParams p) {
                                reinterpret_cast<lds_char*>((__attribute__((address_space(3))) char*)smem));
 }
 
-// Log-sum-exp merge of a split prefill's parts: thread (row, head, 4 dims).
+// Log-sum-exp merge of a split prefill's S parts: thread (row, head, 4 dims).
+// S is a template argument so that the parts' loads are all issued before
+// their first use, in exactly S registers' worth of values.
+template <int S>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
     const int D4 = p.head_dim / 4;
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -53,25 +56,23 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
     if (row >= p.q_start[p.num_chunks]) return;
     const int rem = (int)(idx - row * per_row);
     const int head = rem / D4, d4 = rem - head * D4;
-    // One pass, all parts' loads issued together; parts with an empty key
-    // range (sum 0) weigh 0.
-    float2 ml[kMaxPrefillSplits];
-    float4 v[kMaxPrefillSplits];
+    float2 ml[S];
+    float4 v[S];
     float M = -__builtin_inff();
 #pragma unroll
-    for (int s = 0; s < kMaxPrefillSplits; ++s) {
-        if (s < p.splits) {
-            const int64_t rh = ((int64_t)s * p.rows_cap + row) * p.num_heads + head;
-            ml[s] = p.ws_ml[rh];
-            v[s] = reinterpret_cast<const float4*>(p.ws_o + rh * p.head_dim)[d4];
-            if (ml[s].y > 0.f) M = fmaxf(M, ml[s].x);
-        }
+    for (int s = 0; s < S; ++s) {
+        const int64_t rh = ((int64_t)s * p.rows_cap + row) * p.num_heads + head;
+        ml[s] = p.ws_ml[rh];
+        v[s] = reinterpret_cast<const float4*>(p.ws_o + rh * p.head_dim)[d4];
     }
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+        if (ml[s].y > 0.f) M = fmaxf(M, ml[s].x);  // parts with no visible key (sum 0) weigh 0
     float L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int s = 0; s < kMaxPrefillSplits; ++s) {
-        if (s < p.splits && ml[s].y > 0.f) {
+    for (int s = 0; s < S; ++s) {
+        if (ml[s].y > 0.f) {
             const float w = exp2f(ml[s].x - M);
             L += w * ml[s].y;
             acc.x += w * v[s].x;
@@ -84,6 +85,16 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
     reinterpret_cast<float4*>(p.out + ((int64_t)row * p.num_heads + head) * p.head_dim)[d4] =
         make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
 }
+
+template <int S>
+hipError_t launch_merge_s(const PrefillParams& p, hipStream_t stream) {
+    if (p.splits != S) return launch_merge_s<S - 1>(p, stream);
+    const int64_t threads = (int64_t)p.rows_cap * p.num_heads * (p.head_dim / 4);
+    hipLaunchKernelGGL(prefill_merge_kernel<S>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+template <>
+hipError_t launch_merge_s<1>(const PrefillParams&, hipStream_t) { return hipErrorInvalidValue; }
 
 template <int KV, int D>
 hipError_t launch_dma(const PrefillParams& p, hipStream_t stream) {
@@ -156,9 +167,8 @@ hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream) {
 #undef VCPP_PF_D
     if (err != hipSuccess) return err;
     if (p.splits > 1) {
-        const int64_t threads = (int64_t)p.rows_cap * p.num_heads * (p.head_dim / 4);
-        hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, p);
-        err = hipGetLastError();
+        if (p.splits > kMaxPrefillSplits) return hipErrorInvalidValue;
+        err = launch_merge_s<kMaxPrefillSplits>(p, stream);
         if (err != hipSuccess) return err;
     }
     if (prof) prof_end(kKernelPrefill, stream);
