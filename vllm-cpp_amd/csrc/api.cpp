@@ -96,11 +96,17 @@ int device_cus() {
 // that use them hold g_fork_mu from the fork to the join's enqueue.
 std::mutex g_fork_mu;
 
-const vcpp::MergeFork* merge_fork() {
+const vcpp::MergeFork* merge_fork(hipStream_t stream) {
     static vcpp::MergeFork mf[64];
     static int state[64] = {};  // 0 not made, 1 made, -1 failed
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    // Only for a stream of the current device (the side stream is made there).
+    hipDevice_t sdev = -1;
+    if (stream && (hipStreamGetDevice(stream, &sdev) != hipSuccess || sdev != dev)) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
     if (state[dev] == 0) {
         bool ok = hipStreamCreateWithFlags(&mf[dev].side, hipStreamNonBlocking) == hipSuccess;
         ok = ok && hipEventCreateWithFlags(&mf[dev].fork, hipEventDisableTiming) == hipSuccess;
@@ -683,7 +689,7 @@ int vcpp_paged_mixed_step(const vcpp_kv_pages* kv, const float* dq, float* dout,
                                                       q_start, prefix_lens, num_chunks, max_chunk_len, num_heads);
         const hipStream_t s = static_cast<hipStream_t>(stream);
         std::lock_guard<std::mutex> lock(g_fork_mu);
-        const vcpp::MergeFork* mf = merge_fork();
+        const vcpp::MergeFork* mf = merge_fork(s);
         hipError_t e = vcpp::launch_decode(dp, s, mf);
         if (e != hipSuccess) return hip_fail(e, "decode launch");
         e = vcpp::launch_prefill(pp, s);
