@@ -101,3 +101,28 @@ def test_mixed_one_side_empty(cuda):
     assert_close(out_d.cpu().numpy(), O.decode(pool, qd, dtab, dctx, 64), ATOL, RTOL, what="mixed decode only")
     assert_close(out_p.cpu().numpy(), O.prefill(pool, qp.astype(np.float32), ptab, q_start, pre, 64),
                  ATOL, RTOL, what="mixed prefill only")
+
+
+@pytest.mark.parametrize("case", range(6))
+def test_mixed_random(cuda, case):
+    """Seeded random steps through the default path (decode, then the prefill
+    beside the decode's merge on the side stream): page dtype, heads, head
+    dim, ragged decode contexts and prefill chunks drawn together."""
+    rng = np.random.default_rng(9100 + case)
+    kind = int(rng.choice([O.ORC_F16, O.ORC_I8, O.ORC_FP8]))
+    H, Hkv = [(64, 8), (32, 4), (16, 2), (24, 8)][int(rng.integers(4))]
+    D = int(rng.choice([64, 80, 128]))
+    nd = int(rng.integers(1, 40))
+    dctx = rng.integers(0, 3000, nd)
+    dctx[rng.random(nd) < 0.1] = 0
+    nc = int(rng.integers(1, 5))
+    prefix = rng.integers(0, 1500, nc)
+    chunk = rng.integers(1, 200, nc)
+    print("mixed case %d: kind %d H %d Hkv %d D %d decodes %d (tokens %d) chunks %s prefixes %s"
+          % (case, kind, H, Hkv, D, nd, int(dctx.sum()), list(chunk), list(prefix)), flush=True)
+    pool, dctx, dtab, qd, ptab, q_start, pre, qp = mixed_case(kind, 9200 + case, list(dctx), list(prefix),
+                                                              list(chunk), H, Hkv, D)
+    got_d, got_p = run_mixed(pool, dctx, dtab, qd, ptab, q_start, pre, qp, H, fused=False)
+    assert_close(got_d, O.decode(pool, qd, dtab, dctx, H), ATOL, RTOL, what="mixed random %d decode" % case)
+    assert_close(got_p, O.prefill(pool, qp.astype(np.float32), ptab, q_start, pre, H), ATOL, RTOL,
+                 what="mixed random %d prefill" % case)
