@@ -371,6 +371,20 @@ void test_attention(KVDtype dt) {
             close(gd.data(), want.data(), gd.size(), tol, rtol, "paged_attention_step decodes, host buffers");
             close(g1s.data(), w1.data(), g1s.size(), tol, rtol, "paged_attention_step chunk 0, host buffers");
             close(gcs.data(), wc.data(), gcs.size(), tol, rtol, "paged_attention_step chunk 1, host buffers");
+            // the same step on device buffers (queued on the pool's stream)
+            CHECK(hipMemset(od, 0xFF, q.size() * 4) == hipSuccess && hipMemset(o1d, 0xFF, q1.size() * 4) == hipSuccess &&
+                      hipMemset(ocd, 0xFF, qc.size() * 4) == hipSuccess,
+                  "poison");
+            paged_attention_step(qp, tp, sl, opp, {{q1d, &tables[1], 0, n1, o1d}, {qcd, &tables[3], pre, n, ocd}},
+                                 m.block_pool(), H, HKV, D, layer);
+            CHECK(hipDeviceSynchronize() == hipSuccess, "sync");
+            CHECK(hipMemcpy(gd.data(), od, gd.size() * 4, hipMemcpyDeviceToHost) == hipSuccess &&
+                      hipMemcpy(g1s.data(), o1d, g1s.size() * 4, hipMemcpyDeviceToHost) == hipSuccess &&
+                      hipMemcpy(gcs.data(), ocd, gcs.size() * 4, hipMemcpyDeviceToHost) == hipSuccess,
+                  "copy");
+            close(gd.data(), want.data(), gd.size(), tol, rtol, "paged_attention_step decodes, device buffers");
+            close(g1s.data(), w1.data(), g1s.size(), tol, rtol, "paged_attention_step chunk 0, device buffers");
+            close(gcs.data(), wc.data(), gcs.size(), tol, rtol, "paged_attention_step chunk 1, device buffers");
         }
         for (float* p : {q1d, o1d, qcd, ocd}) (void)hipFree(p);
     }
