@@ -1020,9 +1020,39 @@ __device__ __forceinline__ void decode_page_body(const DecodeParams& p, int bx, 
     // preceded by X units that hold no tile (the cost of starting it), and
     // each range's bounds map back to real tile indices a, b.
     const int X = p.switch_tiles;
+    // Context lengths of the first 128 sequences stay in registers (lane l:
+    // sequences l and 64 + l) from this first scan on: every later scan (the
+    // range bounds, the empty-sequence zeroing, the tile list) reads them
+    // from there instead of with a dependent round trip to memory of its own.
+    int ctx_c0 = 0, ctx_c1 = 0, tl_c0 = 0, tl_c1 = 0;
+    auto lane_ctx = [&](int base) -> int {  // context length of sequence base + lane
+        if (base == 0) return ctx_c0;
+        if (base == 64) return ctx_c1;
+        const int sl = base + lane;
+        return sl < p.num_seqs ? min(max(p.context_lens[sl], 0), p.ctx_cap) : 0;
+    };
+    auto load_tlen = [&](int base) -> int {  // usable table length of sequence base + lane
+        const int sl = base + lane;
+        return sl < p.num_seqs && p.table_lens ? min(p.max_blocks, p.table_lens[sl]) : p.max_blocks;
+    };
+    auto lane_tlen = [&](int base) -> int {
+        if (base == 0) return tl_c0;
+        if (base == 64) return tl_c1;
+        return load_tlen(base);
+    };
     int T = 0, K = 0;
     for (int base = 0; base < p.num_seqs; base += 64) {
-        const int nt = base + lane < p.num_seqs ? tiles_of(p, base + lane) : 0;
+        const int sl = base + lane;
+        const int ctx = sl < p.num_seqs ? min(max(p.context_lens[sl], 0), p.ctx_cap) : 0;
+        if (base == 0) {
+            ctx_c0 = ctx;
+            tl_c0 = load_tlen(0);
+        }
+        if (base == 64) {
+            ctx_c1 = ctx;
+            tl_c1 = load_tlen(64);
+        }
+        const int nt = (ctx + kTile - 1) / kTile;
         T += wave_sum(nt);
         K += wave_sum(nt > 0 ? 1 : 0);
     }
@@ -1033,8 +1063,7 @@ __device__ __forceinline__ void decode_page_body(const DecodeParams& p, int bx, 
         if (V >= Tv) return T;
         int cs = 0, ck = 0;
         for (int base = 0; base < p.num_seqs; base += 64) {
-            const int sl = base + lane;
-            const int nt = sl < p.num_seqs ? tiles_of(p, sl) : 0;
+            const int nt = (lane_ctx(base) + kTile - 1) / kTile;
             const int Sl = cs + wave_excl_scan(nt, lane);
             const int kl = ck + wave_excl_scan(nt > 0 ? 1 : 0, lane);
             const int vfirst = Sl + X * (kl + 1);  // virtual position of its first tile
@@ -1057,7 +1086,7 @@ __device__ __forceinline__ void decode_page_body(const DecodeParams& p, int bx, 
         int carry = 0;
         for (int base = 0; base < p.num_seqs; base += 64) {
             const int sl = base + lane;
-            const int nt = sl < p.num_seqs ? tiles_of(p, sl) : 0;
+            const int nt = (lane_ctx(base) + kTile - 1) / kTile;
             const int Sl = carry + wave_excl_scan(nt, lane);
             carry += wave_sum(nt);
             const bool zero_here = sl < p.num_seqs && nt == 0 &&
@@ -1420,8 +1449,8 @@ __device__ __forceinline__ void decode_page_body(const DecodeParams& p, int bx, 
                 // length, loaded together; the sequences the window overlaps
                 // read them by lane below instead of with loads of their own.
                 const bool in = sl < p.num_seqs;
-                const int ctx_l = in ? min(max(p.context_lens[sl], 0), p.ctx_cap) : 0;
-                const int tlen_l = in && p.table_lens ? min(p.max_blocks, p.table_lens[sl]) : p.max_blocks;
+                const int ctx_l = lane_ctx(base);
+                const int tlen_l = lane_tlen(base);
                 const int nt = (ctx_l + kTile - 1) / kTile;
                 const int Sl = carry + wave_excl_scan(nt, lane);
                 carry += wave_sum(nt);
