@@ -254,22 +254,35 @@ __device__ __forceinline__ int range_start(int w, int T, int G) {
     return (int)(((int64_t)w * T) / G);
 }
 
+// Cross-lane steps on DPP (VALU, no LDS round trip): lanes whose source is
+// outside its row, or whose row / bank is masked off, read 0.
+template <int CTRL, int ROW_MASK = 0xF, int BANK_MASK = 0xF>
+__device__ __forceinline__ int dpp_or0(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, BANK_MASK, false);
+}
+
+// Inclusive prefix sum over the wave's 64 lanes: Hillis-Steele within each
+// row of 16 (row_shr 1, 2, 4, 8), then row 0's total into row 1 and row 2's
+// into row 3 (row_bcast:15), then rows 0-1's total into rows 2 and 3
+// (row_bcast:31).
+__device__ __forceinline__ int wave_incl_scan(int x) {
+    x += dpp_or0<0x111>(x);
+    x += dpp_or0<0x112>(x);
+    x += dpp_or0<0x114>(x);
+    x += dpp_or0<0x118>(x);
+    x += dpp_or0<0x142, 0xA>(x);
+    x += dpp_or0<0x143, 0xC>(x);
+    return x;
+}
+
 // Sum over the wave's lanes, returned as a scalar (provably uniform).
 __device__ __forceinline__ int wave_sum(int x) {
-#pragma unroll
-    for (int k = 32; k >= 1; k >>= 1) x += __shfl_xor(x, k, 64);
-    return __builtin_amdgcn_readfirstlane(x);
+    return __builtin_amdgcn_readlane(wave_incl_scan(x), 63);
 }
 
 // Exclusive prefix sum over the wave's lanes.
-__device__ __forceinline__ int wave_excl_scan(int x, int lane) {
-    int y = x;
-#pragma unroll
-    for (int k = 1; k < 64; k <<= 1) {
-        const int t = __shfl_up(y, k, 64);
-        if (lane >= k) y += t;
-    }
-    return y - x;
+__device__ __forceinline__ int wave_excl_scan(int x, int /*lane*/) {
+    return wave_incl_scan(x) - x;
 }
 
 // Range holding tile t (0 <= t < T): the largest w with floor(w T / G) <= t.
