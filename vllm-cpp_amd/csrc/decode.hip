@@ -1013,6 +1013,13 @@ __device__ __forceinline__ void decode_page_body(const DecodeParams& p, int bx, 
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
+    // Every argument the range start reads, in scalar registers before the
+    // first use: one batch of kernel-argument loads and one wait, instead of
+    // a load and a wait wherever the compiler first needs a field.
+    asm volatile("" ::"s"(p.context_lens), "s"(p.table_lens), "s"(p.block_tables), "s"(p.q), "s"(p.out),
+                 "s"(p.num_seqs), "s"(p.ctx_cap), "s"(p.max_blocks), "s"(p.num_wg), "s"(p.switch_tiles),
+                 "s"(p.block_size), "s"(p.num_blocks), "s"(p.num_heads), "s"(p.group), "s"(p.k), "s"(p.v),
+                 "s"(p.block_stride));
     // Ranges of the split: G in all.  Workgroup w walks the contiguous ranges
     // [r_lo, r_hi) with one DMA ring: one range for the balanced split; with
     // fixed partitions (G > workgroups, no switch units) a run of whole
@@ -1053,19 +1060,24 @@ __device__ __forceinline__ void decode_page_body(const DecodeParams& p, int bx, 
         if (base == 64) return tl_c1;
         return load_tlen(base);
     };
+    {
+        // The first 128 sequences' lengths: four loads with clamped indices
+        // in one batch, one wait.
+        const int n1 = max(p.num_seqs - 1, 0);
+        const int r0 = p.context_lens[min(lane, n1)], r1 = p.context_lens[min(64 + lane, n1)];
+        int u0 = p.max_blocks, u1 = p.max_blocks;
+        if (p.table_lens) {
+            u0 = p.table_lens[min(lane, n1)];
+            u1 = p.table_lens[min(64 + lane, n1)];
+        }
+        ctx_c0 = lane < p.num_seqs ? min(max(r0, 0), p.ctx_cap) : 0;
+        ctx_c1 = 64 + lane < p.num_seqs ? min(max(r1, 0), p.ctx_cap) : 0;
+        tl_c0 = lane < p.num_seqs ? min(p.max_blocks, u0) : p.max_blocks;
+        tl_c1 = 64 + lane < p.num_seqs ? min(p.max_blocks, u1) : p.max_blocks;
+    }
     int T = 0, K = 0;
     for (int base = 0; base < p.num_seqs; base += 64) {
-        const int sl = base + lane;
-        const int ctx = sl < p.num_seqs ? min(max(p.context_lens[sl], 0), p.ctx_cap) : 0;
-        if (base == 0) {
-            ctx_c0 = ctx;
-            tl_c0 = load_tlen(0);
-        }
-        if (base == 64) {
-            ctx_c1 = ctx;
-            tl_c1 = load_tlen(64);
-        }
-        const int nt = (ctx + kTile - 1) / kTile;
+        const int nt = (lane_ctx(base) + kTile - 1) / kTile;
         T += wave_sum(nt);
         K += wave_sum(nt > 0 ? 1 : 0);
     }
