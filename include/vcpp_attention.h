@@ -167,7 +167,12 @@ int vcpp_paged_decode_noalloc(const vcpp_kv_pages* kv, const float* q, float* ou
  *   block_tables [num_chunks][max_blocks_per_seq] int32
  *   q_start      [num_chunks + 1] int32 on the device (q_start[0] == 0)
  *   prefix_lens  [num_chunks] int32 on the device
- *   max_chunk_len host-side upper bound of the chunk lengths (sizes the grid)
+ *   max_chunk_len host-side upper bound of the chunk lengths (sizes the grid;
+ *                 a longer chunk is a caller error: rows the grid does not
+ *                 reach -- the chunk's first rows before its last
+ *                 max_chunk_len, rounded to whole query tiles, and in
+ *                 vcpp_paged_prefill_split also rows past num_chunks *
+ *                 max_chunk_len -- are left unwritten, never garbage)
  * KV dtypes: VCPP_KV_F16, VCPP_KV_I8 and VCPP_KV_FP8 (byte pages are widened to fp16 on the
  * way into LDS: FP8 to its values; int8 K to exact integers whose per-key scale multiplies the
  * score in fp32, int8 V to fp16(v * scale), one rounding); head_dim 64, 80 or 128;
@@ -213,11 +218,13 @@ size_t vcpp_prefill_workspace_size(const vcpp_kv_pages* kv, int32_t num_chunks, 
  * num_chunks / max_chunk_len) over the same pages, with the same results.
  * By default the decode kernel and then the prefill kernel run on `stream`;
  * when both sides are present, the decode's split-K merge runs on a
- * library-owned side stream (default priority, one per device) that waits
- * for the decode kernel by an event, so that it overlaps the prefill, and
- * `stream` waits for it by another event before the call returns: all
- * results are ordered on `stream` as with the two separate calls
- * (VCPP_NO_MERGE_FORK=1 keeps the merge on `stream`).  With
+ * library-owned side stream (default priority, one per device and caller
+ * stream, so steps on different streams never share one, also under graph
+ * capture) that waits for the decode kernel by an event, so that it overlaps
+ * the prefill, and `stream` waits for it by another event before the call
+ * returns, also when a later launch fails: all results are ordered on
+ * `stream` as with the two separate calls (VCPP_NO_MERGE_FORK=1 keeps the
+ * merge on `stream`).  With
  * VCPP_MIXED_FUSED=1, where the shape allows (fp16, int8 or FP8 pages;
  * head_dim 64 or 80; num_kv_heads a multiple of 4; <= 8 query heads per kv
  * head; a CU count that is a multiple of 8), both run in ONE launch that

@@ -455,6 +455,84 @@ void test_two_pools_two_streams() {
     (void)hipStreamDestroy(st[1]);
 }
 
+
+// read_kv_prefill on rows whose byte count is not a multiple of 4 (FP8 and
+// FP16 pools of odd kv_dim) and on an INT8 pool with more kv heads (300) than
+// the gather's workgroup has threads: every byte and scale of each row comes
+// back.  The pages are filled with raw bytes, so the expected rows are the
+// oracle's decode of exactly those bytes.
+void test_read_kv_prefill_odd_rows() {
+    struct Case { KVDtype dt; int32_t kv, hd; const char* name; };
+    const Case cases[] = {{KVDtype::FP8_E4M3, 37, 37, "FP8 kv_dim 37"},
+                          {KVDtype::FP16, 37, 37, "FP16 kv_dim 37"},
+                          {KVDtype::INT8, 300, 1, "INT8 300 kv heads of dim 1"}};
+    for (const Case& cs : cases) {
+        const int32_t L = 2, NB = 4, layer = 1, seq = 40;
+        KVCacheManager m(L, cs.kv, NB, cs.dt, cs.hd);
+        const BlockPool& p = m.block_pool();
+        const int32_t esz = kv_elem_size(cs.dt), hkv = cs.kv / cs.hd;
+        const size_t slab = (size_t)16 * cs.kv * esz;
+        std::mt19937 rng(7);
+        std::vector<std::vector<uint8_t>> kb(NB), vb(NB);
+        std::vector<std::vector<uint16_t>> ksc(NB), vsc(NB);
+        for (int32_t b = 0; b < NB; ++b) {
+            kb[b].resize(slab);
+            vb[b].resize(slab);
+            for (size_t i = 0; i < slab; ++i) {
+                kb[b][i] = (uint8_t)rng();
+                vb[b][i] = (uint8_t)rng();
+            }
+            if (cs.dt == KVDtype::FP8_E4M3)  // keep codes finite (exponent field below 15)
+                for (size_t i = 0; i < slab; ++i) {
+                    kb[b][i] &= 0xF7;
+                    vb[b][i] &= 0xF7;
+                }
+            if (cs.dt == KVDtype::FP16)  // finite halves: clear the top exponent bit
+                for (size_t i = 1; i < slab; i += 2) {
+                    kb[b][i] &= 0xBF;
+                    vb[b][i] &= 0xBF;
+                }
+            CHECK(hipMemcpy(const_cast<uint8_t*>(p.get_k_raw(b, layer)), kb[b].data(), slab, hipMemcpyHostToDevice) == hipSuccess, "fill K");
+            CHECK(hipMemcpy(const_cast<uint8_t*>(p.get_v_raw(b, layer)), vb[b].data(), slab, hipMemcpyHostToDevice) == hipSuccess, "fill V");
+            if (cs.dt == KVDtype::INT8) {
+                ksc[b].resize((size_t)hkv * 16);
+                vsc[b].resize((size_t)hkv * 16);
+                for (size_t i = 0; i < ksc[b].size(); ++i) {
+                    ksc[b][i] = (uint16_t)(0x2000 + (rng() & 0x1FFF));  // positive normal halves
+                    vsc[b][i] = (uint16_t)(0x2000 + (rng() & 0x1FFF));
+                }
+                const vcpp_kv_pages pg = p.pages(layer);
+                CHECK(hipMemcpy(const_cast<uint16_t*>(pg.k_scale) + b * pg.scale_block_stride, ksc[b].data(), ksc[b].size() * 2, hipMemcpyHostToDevice) == hipSuccess, "fill K scales");
+                CHECK(hipMemcpy(const_cast<uint16_t*>(pg.v_scale) + b * pg.scale_block_stride, vsc[b].data(), vsc[b].size() * 2, hipMemcpyHostToDevice) == hipSuccess, "fill V scales");
+            }
+        }
+        const std::vector<int32_t> table = {2, 0, 3};  // 40 positions over 3 blocks
+        std::vector<float> rk((size_t)seq * cs.kv, -7.f), rv((size_t)seq * cs.kv, -7.f);
+        read_kv_prefill(p, table, seq, layer, hkv, cs.hd, rk.data(), rv.data());
+        for (int32_t pos = 0; pos < seq; ++pos) {
+            const int32_t b = table[pos / 16], slot = pos % 16;
+            for (int32_t j = 0; j < cs.kv; ++j) {
+                const size_t e = (size_t)slot * cs.kv + j;
+                float wk, wv;
+                if (cs.dt == KVDtype::FP8_E4M3) {
+                    wk = orc_fp8_decode(kb[b][e]);
+                    wv = orc_fp8_decode(vb[b][e]);
+                } else if (cs.dt == KVDtype::FP16) {
+                    wk = orc_f16_decode((uint16_t)(kb[b][2 * e] | kb[b][2 * e + 1] << 8));
+                    wv = orc_f16_decode((uint16_t)(vb[b][2 * e] | vb[b][2 * e + 1] << 8));
+                } else {
+                    const int32_t h = j / cs.hd;
+                    wk = (float)(int8_t)kb[b][e] * orc_f16_decode(ksc[b][h * 16 + slot]);
+                    wv = (float)(int8_t)vb[b][e] * orc_f16_decode(vsc[b][h * 16 + slot]);
+                }
+                CHECK(rk[(size_t)pos * cs.kv + j] == wk && rv[(size_t)pos * cs.kv + j] == wv,
+                      "%s: read_kv_prefill pos %d dim %d", cs.name, pos, j);
+            }
+        }
+        std::printf("ok   read_kv_prefill, %-42s (bit-exact)\n", cs.name);
+    }
+}
+
 }  // namespace
 
 int main() {
@@ -473,6 +551,7 @@ int main() {
         test_attention(dt);
     }
     test_two_pools_two_streams();
+    test_read_kv_prefill_odd_rows();
     std::printf("ALL PASSED (%d checks)\n", g_checks);
     return 0;
 }

@@ -100,3 +100,52 @@ def test_graph_replays_match_eager(cuda, which):
         torch.cuda.synchronize()
         for o in outs:
             assert torch.equal(w[o], ref[o]), "%s: replay %d of %s differs from the eager call" % (which, rep, o)
+
+
+def test_mixed_capture_beside_eager_stream(cuda):
+    """One stream captures a mixed step while another stream of the same GPU
+    runs mixed steps eagerly inside the capture: each caller stream forks its
+    merge onto its own side stream, so the eager steps are neither recorded
+    into the graph nor break the capture, and both results match the eager
+    reference (the graph over three replays)."""
+    wa = setup(97)
+    wb = setup(98)
+    wsa = workspace(wa, "mixed")
+    wsb = workspace(wb, "mixed")
+    mixed(wa, wsa)
+    mixed(wb, wsb)
+    torch.cuda.synchronize()
+    ref_a = {o: wa[o].clone() for o in ("dout", "pout")}
+    ref_b = {o: wb[o].clone() for o in ("dout", "pout")}
+    sb = torch.cuda.Stream()
+    sb.wait_stream(torch.cuda.current_stream())
+
+    def mixed_b():
+        pyvcpp.paged_mixed_step(wb["pages"], wb["dq"], wb["dout"], wb["dtab"], wb["dctx"], wb["max_ctx"], wb["pq"],
+                                wb["pout"], wb["ptab"], wb["q_start"], wb["prefix"], wb["max_chunk"], H,
+                                workspace=wsb, stream=sb)
+
+    mixed_b()  # its side stream exists before the capture
+    torch.cuda.synchronize()
+    for o in ("dout", "pout"):
+        wb[o].fill_(float("nan"))
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        mixed(wa, wsa)
+        mixed_b()  # eager, on stream sb, while the capture is open
+        mixed(wa, wsa)
+    torch.cuda.synchronize()
+    for o in ("dout", "pout"):
+        assert torch.equal(wb[o], ref_b[o]), "eager step beside the capture: %s differs" % o
+    for rep in range(3):
+        for o in ("dout", "pout"):
+            wa[o].fill_(float("nan"))
+            wb[o].fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for o in ("dout", "pout"):
+            assert torch.equal(wa[o], ref_a[o]), "replay %d: %s differs" % (rep, o)
+            # nothing of stream b's step was recorded into the graph
+            assert torch.isnan(wb[o]).all(), "replay %d wrote stream b's %s" % (rep, o)

@@ -104,3 +104,32 @@ def test_split_rejects_small_workspace(cuda):
     with pytest.raises(RuntimeError):
         pyvcpp.paged_prefill_split(dp.pages, dev(q16), out, dev(tables), dev(q_start), dev(pre), 16, 6000, 8,
                                    workspace=ws)
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_chunk_longer_than_max_chunk_len(cuda, split):
+    """A caller error: chunk 0 holds 200 rows but max_chunk_len says 64.
+    Rows the grid does not reach keep their previous contents (NaN here),
+    every other row equals the oracle; the split path's merge does not write
+    stale workspace rows into the uncovered ones."""
+    prefix, chunk = [4000, 3000], [200, 40]
+    pool, q16, q32, tables, q_start, pre = make_case(O.ORC_F16, 760, prefix, chunk, 16, 2)
+    dp = DevPool(pool)
+    out = torch.full(q16.shape, float("nan"), dtype=torch.float32, device="cuda:0")
+    args = (dp.pages, dev(q16), out, dev(np.asarray(tables, np.int32)), dev(np.asarray(q_start, np.int32)),
+            dev(np.asarray(pre, np.int32)), 64)
+    if split:
+        need = pyvcpp.prefill_workspace_size(dp.pages, 2, 64, 4000, 16)
+        assert need > 0
+        ws = torch.full((need,), 0x3f, dtype=torch.uint8, device="cuda:0")  # stale finite values
+        pyvcpp.paged_prefill_split(*args, 4000, 16, workspace=ws)
+    else:
+        pyvcpp.paged_prefill(*args, 16)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    want = O.prefill(pool, q32, tables, q_start, pre, 16)
+    rows_nan = np.isnan(got).all(axis=(1, 2))
+    assert (np.isnan(got).any(axis=(1, 2)) == rows_nan).all(), "a row is partly written"
+    assert rows_nan[:128].all(), "rows before the chunk's reachable tiles were written"
+    assert not rows_nan[192:200].any(), "the chunk's last tile was not computed"
+    assert_close(got[~rows_nan], want[~rows_nan], ATOL, RTOL, what="written rows, split=%s" % split)

@@ -11,6 +11,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -91,30 +92,41 @@ int device_cus() {
     return cus[dev];
 }
 
-// The mixed step's side stream (default priority) and fork / join events,
-// one set per device, made on first use and kept for the process.  Calls
-// that use them hold g_fork_mu from the fork to the join's enqueue.
+// The mixed step's side streams (default priority) and fork / join events:
+// one set per (device, caller stream), made on first use and kept for the
+// process.  Each caller stream forks onto its own side stream, so steps on
+// different streams never share one (a side stream joined to one stream's
+// graph capture is never used by another stream meanwhile).  Calls on one
+// stream are serialised by the caller, as for every entry point; g_fork_mu
+// guards only the table.
 std::mutex g_fork_mu;
 
 const vcpp::MergeFork* merge_fork(hipStream_t stream) {
-    static vcpp::MergeFork mf[64];
-    static int state[64] = {};  // 0 not made, 1 made, -1 failed
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return nullptr;
     // Only for a stream of the current device (the side stream is made there).
     hipDevice_t sdev = -1;
     if (stream && (hipStreamGetDevice(stream, &sdev) != hipSuccess || sdev != dev)) {
         (void)hipGetLastError();
         return nullptr;
     }
-    if (state[dev] == 0) {
-        bool ok = hipStreamCreateWithFlags(&mf[dev].side, hipStreamNonBlocking) == hipSuccess;
-        ok = ok && hipEventCreateWithFlags(&mf[dev].fork, hipEventDisableTiming) == hipSuccess;
-        ok = ok && hipEventCreateWithFlags(&mf[dev].join, hipEventDisableTiming) == hipSuccess;
-        state[dev] = ok ? 1 : -1;
+    struct Entry {
+        vcpp::MergeFork mf;
+        bool ok;
+    };
+    static std::map<std::pair<int, hipStream_t>, Entry> table;
+    std::lock_guard<std::mutex> lock(g_fork_mu);
+    auto it = table.find({dev, stream});
+    if (it == table.end()) {
+        Entry en{};
+        bool ok = hipStreamCreateWithFlags(&en.mf.side, hipStreamNonBlocking) == hipSuccess;
+        ok = ok && hipEventCreateWithFlags(&en.mf.fork, hipEventDisableTiming) == hipSuccess;
+        ok = ok && hipEventCreateWithFlags(&en.mf.join, hipEventDisableTiming) == hipSuccess;
         if (!ok) (void)hipGetLastError();
+        en.ok = ok;
+        it = table.emplace(std::make_pair(dev, stream), en).first;
     }
-    return state[dev] == 1 ? &mf[dev] : nullptr;
+    return it->second.ok ? &it->second.mf : nullptr;
 }
 
 // VCPP_NO_MERGE_FORK=1: the mixed step's merge stays on the caller's stream
@@ -688,16 +700,17 @@ int vcpp_paged_mixed_step(const vcpp_kv_pages* kv, const float* dq, float* dout,
         const vcpp::PrefillParams pp = prefill_params(kv, pq, pout, p_block_tables, p_max_blocks_per_seq,
                                                       q_start, prefix_lens, num_chunks, max_chunk_len, num_heads);
         const hipStream_t s = static_cast<hipStream_t>(stream);
-        std::lock_guard<std::mutex> lock(g_fork_mu);
         const vcpp::MergeFork* mf = merge_fork(s);
-        hipError_t e = vcpp::launch_decode(dp, s, mf);
+        bool forked = false;
+        hipError_t e = vcpp::launch_decode(dp, s, mf, &forked);
+        // Once the merge is forked, the caller's stream joins it whatever
+        // fails later, so the stream stays ordered after the merge (and a
+        // capture ends with the side stream joined).
+        const hipError_t ep = e == hipSuccess ? vcpp::launch_prefill(pp, s) : hipSuccess;
+        const hipError_t ej = forked ? hipStreamWaitEvent(s, mf->join, 0) : hipSuccess;
         if (e != hipSuccess) return hip_fail(e, "decode launch");
-        e = vcpp::launch_prefill(pp, s);
-        if (e != hipSuccess) return hip_fail(e, "prefill launch");
-        if (mf) {
-            e = hipStreamWaitEvent(s, mf->join, 0);
-            if (e != hipSuccess) return hip_fail(e, "merge join");
-        }
+        if (ep != hipSuccess) return hip_fail(ep, "prefill launch");
+        if (ej != hipSuccess) return hip_fail(ej, "merge join");
         return VCPP_OK;
     }
     if (fg == 0) {  // two launches on the stream: decode, then prefill

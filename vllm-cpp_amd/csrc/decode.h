@@ -65,11 +65,14 @@ struct DecodeParams {
 // kernel, `fork` is recorded on the launch stream and `side` waits for it;
 // the merge runs on `side`, which records `join` after it.  The caller makes
 // its stream wait for `join` before anything that reads the outputs.
+// *forked (if given) is set once `side` waits on `fork`; from then on `join`
+// is recorded on `side` even when the merge launch fails.
 struct MergeFork {
     hipStream_t side;
     hipEvent_t fork, join;
 };
-hipError_t launch_decode(const DecodeParams& p, hipStream_t stream, const MergeFork* mf = nullptr);
+hipError_t launch_decode(const DecodeParams& p, hipStream_t stream, const MergeFork* mf = nullptr,
+                         bool* forked = nullptr);
 
 // The fused mixed step: one launch of 3 workgroups per CU (cus a multiple of
 // 8), two prefill workers and one decode worker on each CU, then the decode

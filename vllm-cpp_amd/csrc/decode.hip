@@ -1691,7 +1691,7 @@ int decode_group_count(int pairs) {
     return (pairs + wpw - 1) / wpw;
 }
 
-hipError_t launch_decode(const DecodeParams& p, hipStream_t stream, const MergeFork* mf) {
+hipError_t launch_decode(const DecodeParams& p, hipStream_t stream, const MergeFork* mf, bool* forked) {
     if (p.num_seqs == 0) return hipSuccess;
     hipError_t err;
     const bool prof = prof_enabled();
@@ -1752,6 +1752,7 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream, const MergeF
         err = hipEventRecord(mf->fork, stream);
         if (err == hipSuccess) err = hipStreamWaitEvent(mf->side, mf->fork, 0);
         if (err != hipSuccess) return err;
+        if (forked) *forked = true;
         stream = mf->side;
     }
     if (prof) prof_begin(kKernelMerge, stream);
@@ -1763,7 +1764,10 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream, const MergeF
     }
     err = hipGetLastError();
     if (prof) prof_end(kKernelMerge, stream);
-    if (err == hipSuccess && mf) err = hipEventRecord(mf->join, stream);
+    if (mf) {  // recorded even after a failed merge launch, so the caller can always join
+        const hipError_t ej = hipEventRecord(mf->join, stream);
+        if (err == hipSuccess) err = ej;
+    }
     return err;
 }
 

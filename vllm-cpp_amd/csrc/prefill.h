@@ -44,6 +44,7 @@ struct PrefillParams {
     float2* ws_ml;     // [splits][rows_cap][num_heads] (max in log2 units, sum)
     uint64_t bs_magic; // ceil(2^40 / block_size): pos / block_size = (pos * bs_magic) >> 40
     int32_t xcd_cus;   // CUs per XCD (0: unknown; no pairing of heavy and light tiles)
+    int32_t tile_rows; // query rows per workgroup tile (set by launch_prefill for the merge)
 #ifdef VCPP_GATHER_DUMP
     int32_t* gather_dump;    // checker builds: [rows][gather_stride][2] (block, slot)
     int64_t gather_stride;
@@ -56,6 +57,7 @@ hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream);
 constexpr int kMaxPrefillSplits = 16;
 size_t prefill_split_bytes(int splits, int rows_cap, int num_heads, int head_dim);
 int prefill_head_groups(int group);
+int prefill_tile_rows(int head_dim);
 // Dynamic LDS bytes of the prefill kernel for a table of max_blocks entries.
 size_t prefill_lds_bytes(int kv_dtype, int head_dim, int max_blocks);
 

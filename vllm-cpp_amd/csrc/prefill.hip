@@ -54,6 +54,22 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
     const int64_t per_row = (int64_t)p.num_heads * D4;
     const int row = (int)(idx / per_row);
     if (row >= p.q_start[p.num_chunks]) return;
+    // Rows of a chunk longer than max_chunk_len (a caller error) that no
+    // query tile of the grid covered are left unwritten, as the unsplit
+    // kernel leaves them: the grid covers each chunk's last
+    // ceil(max_chunk_len / tile_rows) tiles.
+    {
+        int lo = 0, hi = p.num_chunks - 1;  // chunk of the row: last c with q_start[c] <= row
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (p.q_start[mid] <= row) lo = mid;
+            else hi = mid - 1;
+        }
+        const int q0 = p.q_start[lo], n = p.q_start[lo + 1] - q0;
+        const int ntile = (n + p.tile_rows - 1) / p.tile_rows;
+        const int first = ntile - (p.max_chunk_len + p.tile_rows - 1) / p.tile_rows;
+        if (first > 0 && row - q0 < first * p.tile_rows) return;
+    }
     const int rem = (int)(idx - row * per_row);
     const int head = rem / D4, d4 = rem - head * D4;
     float2 ml[S];
@@ -124,6 +140,14 @@ hipError_t launch_dma(const PrefillParams& p, hipStream_t stream) {
 
 }  // namespace
 
+int prefill_tile_rows(int head_dim) {
+    switch (head_dim) {
+        case 64: return 16 * PDims<64>::RB;
+        case 80: return 16 * PDims<80>::RB;
+        default: return 16 * PDims<128>::RB;
+    }
+}
+
 int prefill_head_groups(int group) { return (group + kHeadsPerGroup - 1) / kHeadsPerGroup; }
 
 size_t prefill_lds_bytes(int kv_dtype, int head_dim, int max_blocks) {
@@ -168,7 +192,9 @@ hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream) {
     if (err != hipSuccess) return err;
     if (p.splits > 1) {
         if (p.splits > kMaxPrefillSplits) return hipErrorInvalidValue;
-        err = launch_merge_s<kMaxPrefillSplits>(p, stream);
+        PrefillParams pm = p;
+        pm.tile_rows = prefill_tile_rows(p.head_dim);
+        err = launch_merge_s<kMaxPrefillSplits>(pm, stream);
         if (err != hipSuccess) return err;
     }
     if (prof) prof_end(kKernelPrefill, stream);

@@ -620,7 +620,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillParams& p, int bx, int
             const float rowsum = sum_over_groups(lsum[rb]);  // row c
             const int tc = t0 + 16 * rb + c;
             // (rows past rows_cap -- chunks longer than max_chunk_len, a
-            // caller error -- are not stored; their output stays unwritten)
+            // caller error -- are not stored, and the merge skips the rows
+            // of such chunks that no tile covered: their output stays
+            // unwritten)
             if (g == 0 && tc < n && q0 + tc < p.rows_cap)
                 p.ws_ml[(pbase + q0 + tc) * p.num_heads + head] = make_float2(m_run[rb], rowsum);
 #pragma unroll

@@ -47,6 +47,30 @@ void decode_rows(const uint8_t* raw, const uint16_t* scales, float* out, int32_t
     }
 }
 
+// Zero n bytes at p: 16-byte stores over the aligned middle, byte stores at
+// the ends.  Pool pages are cleared with this kernel rather than with
+// hipMemsetAsync, so a step that frees or resets blocks can be recorded in a
+// HIP graph (a memset node recorded there has given wrong results on replays).
+__global__ void zero_bytes_kernel(uint8_t* p, int64_t n) {
+    const int64_t head = std::min<int64_t>(n, (16 - ((uintptr_t)p & 15)) & 15);
+    const int64_t nv = (n - head) / 16;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint4* v = reinterpret_cast<uint4*>(p + head);
+    for (int64_t i = t; i < nv; i += stride) v[i] = make_uint4(0, 0, 0, 0);
+    const int64_t tail0 = head + nv * 16;
+    if (t < head) p[t] = 0;
+    if (t < n - tail0) p[tail0 + t] = 0;
+}
+
+void zero_bytes(void* p, size_t n, hipStream_t s, const char* what) {
+    if (n == 0) return;
+    const int64_t nv = (int64_t)(n / 16) + 1;
+    const unsigned blocks = (unsigned)std::min<int64_t>((nv + 255) / 256, 4096);
+    hipLaunchKernelGGL(zero_bytes_kernel, dim3(blocks), dim3(256), 0, s, static_cast<uint8_t*>(p), (int64_t)n);
+    check(hipGetLastError(), what);
+}
+
 }  // namespace
 
 // ---- BlockPool --------------------------------------------------------------
@@ -109,12 +133,12 @@ int32_t BlockPool::alloc() {
 
 void BlockPool::zero_block(int32_t id) {
     hipStream_t s = static_cast<hipStream_t>(stream_);
-    check(hipMemsetAsync(k_ + (int64_t)id * block_bytes_, 0, block_bytes_, s), "zero block K");
-    check(hipMemsetAsync(v_ + (int64_t)id * block_bytes_, 0, block_bytes_, s), "zero block V");
+    zero_bytes(k_ + (int64_t)id * block_bytes_, block_bytes_, s, "zero block K");
+    zero_bytes(v_ + (int64_t)id * block_bytes_, block_bytes_, s, "zero block V");
     if (k_scale_) {
         const size_t n = sizeof(uint16_t) * scale_layer_ * num_layers_;
-        check(hipMemsetAsync(k_scale_ + (int64_t)id * scale_layer_ * num_layers_, 0, n, s), "zero scales");
-        check(hipMemsetAsync(v_scale_ + (int64_t)id * scale_layer_ * num_layers_, 0, n, s), "zero scales");
+        zero_bytes(k_scale_ + (int64_t)id * scale_layer_ * num_layers_, n, s, "zero scales");
+        zero_bytes(v_scale_ + (int64_t)id * scale_layer_ * num_layers_, n, s, "zero scales");
     }
 }
 
@@ -255,12 +279,12 @@ void BlockPool::reset() {
     }
     hipStream_t s = static_cast<hipStream_t>(stream_);
     const size_t nb = std::max<size_t>(blocks_.size(), 1);
-    check(hipMemsetAsync(k_, 0, (size_t)block_bytes_ * nb, s), "reset K");
-    check(hipMemsetAsync(v_, 0, (size_t)block_bytes_ * nb, s), "reset V");
+    zero_bytes(k_, (size_t)block_bytes_ * nb, s, "reset K");
+    zero_bytes(v_, (size_t)block_bytes_ * nb, s, "reset V");
     if (k_scale_) {
         const size_t n = sizeof(uint16_t) * scale_layer_ * num_layers_ * nb;
-        check(hipMemsetAsync(k_scale_, 0, n, s), "reset K scales");
-        check(hipMemsetAsync(v_scale_, 0, n, s), "reset V scales");
+        zero_bytes(k_scale_, n, s, "reset K scales");
+        zero_bytes(v_scale_, n, s, "reset V scales");
     }
 }
 

@@ -30,19 +30,28 @@ __global__ void gather_rows_kernel(const uint8_t* k, const uint8_t* v, const uin
     if (i >= n) return;
     const int64_t off = src[2 * i];  // byte offset of the row in the layer's pages
     const int64_t soff = src[2 * i + 1];  // element offset of the row's first scale
-    const int32_t words = row_bytes / 4;
-    const uint32_t* k4 = reinterpret_cast<const uint32_t*>(k + off);
-    const uint32_t* v4 = reinterpret_cast<const uint32_t*>(v + off);
-    uint32_t* dk = reinterpret_cast<uint32_t*>(dst + (int64_t)i * row_bytes);
-    uint32_t* dv = reinterpret_cast<uint32_t*>(dst + ((int64_t)n + i) * row_bytes);
-    for (int32_t w = threadIdx.x; w < words; w += blockDim.x) {
-        dk[w] = k4[w];
-        dv[w] = v4[w];
+    uint8_t* dk = dst + (int64_t)i * row_bytes;
+    uint8_t* dv = dst + ((int64_t)n + i) * row_bytes;
+    if ((row_bytes & 3) == 0) {  // whole 32-bit words (every row offset is then word aligned)
+        const int32_t words = row_bytes / 4;
+        const uint32_t* k4 = reinterpret_cast<const uint32_t*>(k + off);
+        const uint32_t* v4 = reinterpret_cast<const uint32_t*>(v + off);
+        for (int32_t w = threadIdx.x; w < words; w += blockDim.x) {
+            reinterpret_cast<uint32_t*>(dk)[w] = k4[w];
+            reinterpret_cast<uint32_t*>(dv)[w] = v4[w];
+        }
+    } else {  // rows of an odd byte count (FP8 / INT8 with kv_dim % 4 != 0, or odd fp16 rows)
+        for (int32_t b = threadIdx.x; b < row_bytes; b += blockDim.x) {
+            dk[b] = k[off + b];
+            dv[b] = v[off + b];
+        }
     }
-    if (ks && (int32_t)threadIdx.x < hkv) {
+    if (ks) {
         uint16_t* ds = reinterpret_cast<uint16_t*>(dst + 2 * (int64_t)n * row_bytes);
-        ds[(int64_t)i * hkv + threadIdx.x] = ks[soff + threadIdx.x * scale_stride];
-        ds[((int64_t)n + i) * hkv + threadIdx.x] = vs[soff + threadIdx.x * scale_stride];
+        for (int32_t h = threadIdx.x; h < hkv; h += blockDim.x) {
+            ds[(int64_t)i * hkv + h] = ks[soff + h * scale_stride];
+            ds[((int64_t)n + i) * hkv + h] = vs[soff + h * scale_stride];
+        }
     }
 }
 
