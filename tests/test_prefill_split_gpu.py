@@ -111,7 +111,9 @@ def test_chunk_longer_than_max_chunk_len(cuda, split):
     """A caller error: chunk 0 holds 200 rows but max_chunk_len says 64.
     Rows the grid does not reach keep their previous contents (NaN here),
     every other row equals the oracle; the split path's merge does not write
-    stale workspace rows into the uncovered ones."""
+    stale workspace rows into the uncovered ones (its workspace holds rows
+    below num_chunks * max_chunk_len only, so there the rest stay unwritten
+    too)."""
     prefix, chunk = [4000, 3000], [200, 40]
     pool, q16, q32, tables, q_start, pre = make_case(O.ORC_F16, 760, prefix, chunk, 16, 2)
     dp = DevPool(pool)
@@ -131,5 +133,6 @@ def test_chunk_longer_than_max_chunk_len(cuda, split):
     rows_nan = np.isnan(got).all(axis=(1, 2))
     assert (np.isnan(got).any(axis=(1, 2)) == rows_nan).all(), "a row is partly written"
     assert rows_nan[:128].all(), "rows before the chunk's reachable tiles were written"
-    assert not rows_nan[192:200].any(), "the chunk's last tile was not computed"
+    if not split:  # (the split path stores only rows below num_chunks * max_chunk_len = 128)
+        assert not rows_nan[192:200].any(), "the chunk's last tile was not computed"
     assert_close(got[~rows_nan], want[~rows_nan], ATOL, RTOL, what="written rows, split=%s" % split)
