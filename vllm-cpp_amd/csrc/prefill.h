@@ -57,8 +57,14 @@ hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream);
 constexpr int kMaxPrefillSplits = 16;
 size_t prefill_split_bytes(int splits, int rows_cap, int num_heads, int head_dim);
 int prefill_head_groups(int group);
-int prefill_tile_rows(int head_dim);
-// Dynamic LDS bytes of the prefill kernel for a table of max_blocks entries.
+// Whether fp16 pages of this shape run prefill_wide_kernel (128-row tiles)
+// rather than prefill_dma_kernel, and the query rows per workgroup tile of
+// the kernel that serves them.
+bool prefill_uses_wide(int kv_dtype, int head_dim, int block_size);
+int prefill_tile_rows(int kv_dtype, int head_dim, int block_size);
+size_t prefill_ring_bytes(int kv_dtype, int head_dim);
+// Dynamic LDS bytes of the prefill kernel for a table of max_blocks entries
+// (the larger of the two kernels' needs where both serve the dtype).
 size_t prefill_lds_bytes(int kv_dtype, int head_dim, int max_blocks);
 
 }  // namespace vcpp

@@ -2,20 +2,22 @@
 // (query tile, chunk, kv head / head group), the work of prefill_tile
 // (prefill_body.h).
 #include "prefill_body.h"
+#include "prefill_wide.h"
 #include "profile.h"
+
+#include <cstdlib>
 
 namespace vcpp {
 
 namespace {
 
-template <int KV, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void prefill_dma_kernel(PrefillParams p) {
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-    // Workgroups are dealt to the 8 XCDs round-robin by linear id; remap so
-    // that each XCD walks a contiguous range of (tile, chunk, head) ids and
-    // its L2 holds the K/V of the few (chunk, kv head) pairs it is serving.
-    int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+// Workgroups are dealt to the 8 XCDs round-robin by linear id; remap so that
+// each XCD walks a contiguous range of (tile, chunk, head) ids and its L2
+// holds the K/V of the few (chunk, kv head) pairs it is serving.  slots: the
+// workgroups one CU holds at once (a grid of at most slots per CU pairs the
+// k-th heaviest tile of an XCD's share with its k-th lightest on one CU).
+__device__ __forceinline__ void remap_ids(const PrefillParams& p, int slots, int& bx, int& by, int& bz) {
+    bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
     const int nx = gridDim.x, ny = gridDim.y;
     const int total = nx * ny * gridDim.z;
     if ((total & 7) == 0) {
@@ -30,18 +32,35 @@ void prefill_dma_kernel(PrefillParams p) {
         // heaviest tile beside the k-th lightest of the XCD's share.
         // (Grids of several rounds keep heaviest-first order.)
         const int C = p.xcd_cus;
-        if (C > 0 && per > C && per <= 2 * C && j >= C) j = per + C - 1 - j;
+        if (slots == 2 && C > 0 && per > C && per <= 2 * C && j >= C) j = per + C - 1 - j;
 #endif
         const int m = (lin & 7) * per + j;
         bx = m % nx;
         by = (m / nx) % ny;
         bz = m / (nx * ny);
     }
+}
+
+template <int KV, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_dma_kernel(PrefillParams p) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    int bx, by, bz;
+    remap_ids(p, 2, bx, by, bz);
     // z: (key part, kv head, head group)
     const int zh = p.num_kv_heads * p.head_groups;
     const int part = bz / zh;
     prefill_tile<KV, D, false>(p, bx, by, bz - part * zh, part,
                                reinterpret_cast<lds_char*>((__attribute__((address_space(3))) char*)smem));
+}
+
+// fp16 pages at head_dim 64 / 80: 128-row tiles, one wave per SIMD
+// (prefill_wide_run).
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void prefill_wide_kernel(PrefillParams p) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    prefill_wide_run<D>(p, reinterpret_cast<lds_char*>((__attribute__((address_space(3))) char*)smem));
 }
 
 // Log-sum-exp merge of a split prefill's S parts: thread (row, head, 4 dims).
@@ -112,26 +131,53 @@ hipError_t launch_merge_s(const PrefillParams& p, hipStream_t stream) {
 template <>
 hipError_t launch_merge_s<1>(const PrefillParams&, hipStream_t) { return hipErrorInvalidValue; }
 
+// VCPP_PF_WIDE=1: fp16 pages at head_dim 64 / 80 (power-of-two block size)
+// run prefill_wide_kernel instead of prefill_dma_kernel.  Opt-in: on MI355X
+// it measured about 10 % slower on config 3 (read at every launch, so a
+// process can switch).
+bool wide_requested() {
+    const char* e = std::getenv("VCPP_PF_WIDE");
+    return e && e[0] == '1';
+}
+
+template <int KV, int D>
+constexpr bool use_wide_t() { return KV == VCPP_KV_F16 && wide_prefill_ok<D>(); }
+
+bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+
 template <int KV, int D>
 hipError_t launch_dma(const PrefillParams& p, hipStream_t stream) {
-    constexpr int QT = 16 * PDims<D>::RB;
+    const bool wide = prefill_uses_wide(KV, D, p.block_size);
+    const int QT = prefill_tile_rows(KV, D, p.block_size);
     dim3 grid((p.max_chunk_len + QT - 1) / QT, p.num_chunks,
               p.num_kv_heads * p.head_groups * max(p.splits, 1));
-    size_t lds = prefill_lds_bytes(KV, D, p.max_blocks);
+    size_t lds = (wide ? (size_t)WDims<D>::STAGES * DmaDims<D>::STAGE + 1024 : prefill_ring_bytes(KV, D)) +
+                 (size_t)p.max_blocks * 4;
 #ifdef VCPP_PREFILL_LDS_PAD
     lds = std::max<size_t>(lds, VCPP_PREFILL_LDS_PAD);
 #endif
     // Raise the kernel's dynamic LDS limit on this device only when a launch
     // needs more than it was last set to there (the attribute call is a host
     // round trip; the limit is per device).
-    static size_t attr_lds[64] = {};
+    static size_t attr_lds[2][64] = {};
     int dev = 0;
     const bool known = hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64;
-    if (!known || lds > std::max<size_t>(attr_lds[dev], 65536)) {
-        const hipError_t e = hipFuncSetAttribute((const void*)prefill_dma_kernel<KV, D>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const void* fn = (const void*)prefill_dma_kernel<KV, D>;
+    if constexpr (use_wide_t<KV, D>()) {
+        if (wide) fn = (const void*)prefill_wide_kernel<D>;
+    }
+    if (!known || lds > std::max<size_t>(attr_lds[wide][dev], 65536)) {
+        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
-        if (known) attr_lds[dev] = lds;
+        if (known) attr_lds[wide][dev] = lds;
+    }
+    if constexpr (use_wide_t<KV, D>()) {
+        if (wide) {
+            // A 1-D grid of all tiles (ordered by wide_tile_ids).
+            const unsigned tiles = grid.x * grid.y * grid.z;
+            hipLaunchKernelGGL((prefill_wide_kernel<D>), dim3(tiles), dim3(256), lds, stream, p);
+            return hipGetLastError();
+        }
     }
     hipLaunchKernelGGL((prefill_dma_kernel<KV, D>), grid, dim3(256), lds, stream, p);
     return hipGetLastError();
@@ -140,7 +186,12 @@ hipError_t launch_dma(const PrefillParams& p, hipStream_t stream) {
 
 }  // namespace
 
-int prefill_tile_rows(int head_dim) {
+bool prefill_uses_wide(int kv_dtype, int head_dim, int block_size) {
+    return kv_dtype == VCPP_KV_F16 && (head_dim == 64 || head_dim == 80) && pow2(block_size) && wide_requested();
+}
+
+int prefill_tile_rows(int kv_dtype, int head_dim, int block_size) {
+    if (prefill_uses_wide(kv_dtype, head_dim, block_size)) return WDims<80>::QT;
     switch (head_dim) {
         case 64: return 16 * PDims<64>::RB;
         case 80: return 16 * PDims<80>::RB;
@@ -150,7 +201,8 @@ int prefill_tile_rows(int head_dim) {
 
 int prefill_head_groups(int group) { return (group + kHeadsPerGroup - 1) / kHeadsPerGroup; }
 
-size_t prefill_lds_bytes(int kv_dtype, int head_dim, int max_blocks) {
+// LDS of the ring of prefill_dma_kernel.
+size_t prefill_ring_bytes(int kv_dtype, int head_dim) {
     auto ring = [&](auto d) -> size_t {
         constexpr int D = decltype(d)::value;
         if (kv_dtype == VCPP_KV_I8)
@@ -159,13 +211,21 @@ size_t prefill_lds_bytes(int kv_dtype, int head_dim, int max_blocks) {
             return (size_t)ByteDims<D, false>::STAGES * ByteDims<D, false>::STAGE + 2 * (size_t)DmaDims<D>::STAGE;
         return (size_t)DmaDims<D>::STAGES * DmaDims<D>::STAGE;
     };
-    size_t r = 0;
     switch (head_dim) {
-        case 64: r = ring(std::integral_constant<int, 64>{}); break;
-        case 80: r = ring(std::integral_constant<int, 80>{}); break;
-        case 128: r = ring(std::integral_constant<int, 128>{}); break;
+        case 64: return ring(std::integral_constant<int, 64>{});
+        case 80: return ring(std::integral_constant<int, 80>{});
+        case 128: return ring(std::integral_constant<int, 128>{});
         default: return 0;
     }
+}
+
+size_t prefill_lds_bytes(int kv_dtype, int head_dim, int max_blocks) {
+    size_t r = prefill_ring_bytes(kv_dtype, head_dim);
+    if (r == 0) return 0;
+    if (kv_dtype == VCPP_KV_F16 && head_dim == 64)
+        r = std::max<size_t>(r, (size_t)WDims<64>::STAGES * DmaDims<64>::STAGE + 1024);
+    if (kv_dtype == VCPP_KV_F16 && head_dim == 80)
+        r = std::max<size_t>(r, (size_t)WDims<80>::STAGES * DmaDims<80>::STAGE + 1024);
     return r + (size_t)max_blocks * 4;
 }
 
@@ -193,7 +253,7 @@ hipError_t launch_prefill(const PrefillParams& p, hipStream_t stream) {
     if (p.splits > 1) {
         if (p.splits > kMaxPrefillSplits) return hipErrorInvalidValue;
         PrefillParams pm = p;
-        pm.tile_rows = prefill_tile_rows(p.head_dim);
+        pm.tile_rows = prefill_tile_rows(p.kv_dtype, p.head_dim, p.block_size);
         err = launch_merge_s<kMaxPrefillSplits>(pm, stream);
         if (err != hipSuccess) return err;
     }
@@ -208,3 +268,13 @@ size_t prefill_split_bytes(int splits, int rows_cap, int num_heads, int head_dim
 }
 
 }  // namespace vcpp
+
+#ifdef VCPP_PF_TIMING
+// Timing builds only: reads and clears the wide prefill's segment sums.
+extern "C" int vcpp_pf_timing_read(unsigned long long* out) {
+    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(vcpp::g_pf_timing), 16 * sizeof(unsigned long long)) != hipSuccess)
+        return -1;
+    unsigned long long z[16] = {};
+    return hipMemcpyToSymbol(HIP_SYMBOL(vcpp::g_pf_timing), z, sizeof(z)) == hipSuccess ? 0 : -1;
+}
+#endif
