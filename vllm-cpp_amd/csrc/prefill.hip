@@ -12,8 +12,8 @@ namespace vcpp {
 namespace {
 
 // Workgroups are dealt to the 8 XCDs round-robin by linear id; remap so that
-// each XCD walks a contiguous range of (tile, chunk, head) ids and its L2
-// holds the K/V of the few (chunk, kv head) pairs it is serving.  slots: the
+// each XCD walks a contiguous range of (tile, head group, chunk, kv head) ids
+// and its L2 holds the K/V of the (chunk, kv head) pair it is serving.  slots: the
 // workgroups one CU holds at once (a grid of at most slots per CU pairs the
 // k-th heaviest tile of an XCD's share with its k-th lightest on one CU).
 __device__ __forceinline__ void remap_ids(const PrefillParams& p, int slots, int& bx, int& by, int& bz) {
@@ -34,10 +34,18 @@ __device__ __forceinline__ void remap_ids(const PrefillParams& p, int slots, int
         const int C = p.xcd_cus;
         if (slots == 2 && C > 0 && per > C && per <= 2 * C && j >= C) j = per + C - 1 - j;
 #endif
+        // m = tile + nx (head group + HG (chunk + ny (kv head, key part))):
+        // an XCD's consecutive ids are the tiles of both head groups of one
+        // (chunk, kv head), which read the same K/V pages, so its L2 serves
+        // them to all of its concurrently running workgroups.
         const int m = (lin & 7) * per + j;
+        const int HG = p.head_groups;
         bx = m % nx;
-        by = (m / nx) % ny;
-        bz = m / (nx * ny);
+        int r = m / nx;
+        const int hg = r % HG;
+        r /= HG;
+        by = r % ny;
+        bz = (r / ny) * HG + hg;
     }
 }
 
