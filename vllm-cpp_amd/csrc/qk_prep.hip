@@ -188,7 +188,10 @@ __global__ __launch_bounds__(kQkWaves * 64) void qk_prep_lds_kernel(QkPrepParams
 #pragma unroll
     for (int k = 0; k < NK; ++k) {
         const int idx = 64 * k + lane;
-        in[k] = base[min(idx, nq - 1)];  // past the rows: a valid unit, not stored
+        // Non-temporal: each unit is read once and written once (5.92 -> 6.23
+        // TB/s on config 3's tokens; the dense and KV-write kernels measured
+        // slower with it).
+        in[k] = __builtin_nontemporal_load(base + min(idx, nq - 1));  // past the rows: a valid unit, not stored
     }
     if (rot && lane < P) {
         float sn, c;
@@ -264,7 +267,7 @@ __global__ __launch_bounds__(kQkWaves * 64) void qk_prep_lds_kernel(QkPrepParams
 #pragma unroll
     for (int k = 0; k < NK; ++k) {
         const int idx = 64 * k + lane;
-        if (idx < nq) base[idx] = reinterpret_cast<__attribute__((address_space(3))) f4*>(tile)[idx];
+        if (idx < nq) __builtin_nontemporal_store(reinterpret_cast<__attribute__((address_space(3))) f4*>(tile)[idx], base + idx);
     }
 }
 
