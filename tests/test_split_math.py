@@ -150,3 +150,59 @@ def test_partition_spans_config4():
     for w in range(WG):
         a, b = span_start(w, T, G, WG), span_start(w + 1, T, G, WG)
         assert b - a == 128 and a // 2048 == (b - 1) // 2048
+
+
+class Alternating:
+    """Split in decode.hip with alternating range sizes (byte pages at two
+    workgroups per CU): position 2k takes share / 256 of each pair's units,
+    2k + 1 the rest; start(r) = Tv cum(r) / (128 G), cum(r) = 256 (r / 2) +
+    share (r % 2).  rof is the kernel's inverse (an estimate, then steps)."""
+
+    def __init__(self, Tv, G, share):
+        self.Tv, self.G, self.share = Tv, G, share
+
+    def rstart(self, r):
+        cum = (r >> 1) * 256 + (r & 1) * self.share
+        return (self.Tv * cum) // (self.G * 128)
+
+    def rof(self, t):
+        u = (t * self.G * 128) // self.Tv
+        r = (u >> 8) * 2 + (1 if (u & 255) >= self.share else 0)
+        while r + 1 < self.G and self.rstart(r + 1) <= t:
+            r += 1
+        while r > 0 and self.rstart(r) > t:
+            r -= 1
+        return r
+
+    def all_live(self):
+        return self.Tv * min(self.share, 256 - self.share) >= self.G * 128
+
+
+def position(bx, WG):
+    """The axis position of workgroup bx: the first dispatch round (ids
+    below WG / 2) takes the even positions, the second the odd ones."""
+    return 2 * bx if bx < WG // 2 else 2 * (bx - WG // 2) + 1
+
+
+@pytest.mark.parametrize("share", [100, 128, 152, 164, 176, 220])
+def test_alternating_split(share):
+    """rof(t) is the range whose [start, next start) holds t, for every unit
+    of random and edge-case axes; all_live implies no empty range; the
+    workgroup-to-position map is a bijection that gives the last position to
+    the last workgroup (the owner of trailing empty sequences)."""
+    rng = np.random.default_rng(share)
+    cases = [(1, 2), (7, 512), (511, 512), (512, 512), (40000, 512), (16, 8)]
+    cases += [(int(rng.integers(1, 60000)), int(rng.choice([2, 8, 256, 512, 1024]))) for _ in range(30)]
+    for Tv, G in cases:
+        sp = Alternating(Tv, G, share)
+        starts = [sp.rstart(r) for r in range(G + 1)]
+        assert starts[0] == 0 and starts[-1] == Tv
+        assert all(a <= b for a, b in zip(starts, starts[1:]))
+        ts = range(Tv) if Tv <= 3000 else list(rng.integers(0, Tv, 3000)) + [0, Tv - 1]
+        for t in ts:
+            r = sp.rof(int(t))
+            assert starts[r] <= t < starts[r + 1]
+        if sp.all_live():
+            assert all(a < b for a, b in zip(starts, starts[1:]))
+        pos = [position(b, G) for b in range(G)]
+        assert sorted(pos) == list(range(G)) and pos[G - 1] == G - 1 and pos[0] == 0

@@ -68,6 +68,11 @@ constexpr int64_t kMaxRanges = 1 << 20;
 // sweep of 0, 2, 4, 6, 8 on BASELINE config 2 put the step's best at 2; byte
 // pages (half the bytes per tile) measured the same at 2, 3 and 4.
 constexpr int kSwitchTiles = 2;
+// Byte pages' alternating ranges: the first dispatch round's share of each
+// pair of neighbouring ranges, / 256.  On BASELINE config 5 (int8) 152-164
+// gave the step 2.6-2.7 % over equal ranges, on FP8 pages 176 the kernel
+// 3.5 %; 164 sits between.
+constexpr int kRoundShare = 164;
 
 int32_t ceil_div(int64_t a, int64_t b) { return (int32_t)((a + b - 1) / b); }
 
@@ -143,6 +148,7 @@ struct DecodePlan {
     int32_t page_grid = 0;   // page mode: workgroups (one per range, or a run of ranges each)
     int32_t partition = 0;   // fp32: tokens per partition
     int32_t max_parts = 0;   // fp32: partitions per sequence
+    int32_t g1 = 0, g1_share = 0;  // page mode: unequal ranges (see DecodeParams)
     size_t off_o = 0, off_ml = 0, bytes = 0;
 };
 
@@ -217,6 +223,22 @@ DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_he
     // workgroups, each taking a contiguous run of ranges.
     pl.page_grid = pl.page_mode ? (int32_t)std::min<int64_t>(G, fused_grid > 0 ? fused_grid : page_ranges)
                                 : pl.num_wg;
+    // Byte pages at two workgroups per CU: the dispatcher places ids 0 ..
+    // CUs - 1 first, and those start their rings while the second round's
+    // workgroups still build their tile lists.  Ranges alternate in size
+    // along the split axis, the first round's taking kRoundShare / 256 of
+    // each pair of neighbours (VCPP_DECODE_ROUND_SHARE overrides; 128:
+    // equal ranges).
+    if (pl.page_mode && fused_grid == 0 && partition_size == 0 && pl.page_grid == pl.num_wg &&
+        vcpp::decode_page_wg_per_cu(kv->dtype, kv->num_kv_heads, D) == 2 && bytes &&
+        pl.num_wg == page_ranges && pl.num_wg % 2 == 0) {
+        const char* rs = getenv("VCPP_DECODE_ROUND_SHARE");
+        const int share = rs ? atoi(rs) : kRoundShare;
+        if (share > 0 && share < 256 && share != 128) {
+            pl.g1 = pl.num_wg / 2;
+            pl.g1_share = share;
+        }
+    }
     pl.off_o = 0;
     const size_t blocks = (size_t)G * 2 * pairs;  // [range][slot][kv-head slot]
     pl.off_ml = pl.off_o + align256(blocks * 8 * D * sizeof(float));
@@ -448,6 +470,8 @@ vcpp::DecodeParams decode_params(const vcpp_kv_pages* kv, const float* q, float*
     p.num_wg = pl.num_wg;
     p.page_mode = pl.page_mode ? 1 : 0;
     p.page_grid = pl.page_grid;
+    p.g1 = pl.g1;
+    p.g1_share = pl.g1_share;
     // Switch units only for the balanced page split (the merge kernel maps
     // tiles to ranges on the same axis).
     p.switch_tiles = pl.page_mode && partition_size == 0 ? kSwitchTiles : 0;

@@ -55,6 +55,13 @@ struct DecodeParams {
     int32_t pipeline;  // fp16/int8 pipeline shape (tuning; 0 = default)
     int32_t page_mode; // fp16/int8, Hkv 8: 8-wave workgroups staging whole tiles in LDS
     int32_t page_grid; // workgroups that walk the num_wg ranges (page mode: a run each; else num_wg)
+    // Balanced page split (one range per workgroup), g1 > 0: ranges of
+    // alternating size, the even positions of the axis taking g1_share / 256
+    // of each neighbouring pair; workgroup w < num_wg / 2 walks position 2 w,
+    // the others position 2 (w - num_wg / 2) + 1 (g1 == 0: equal ranges,
+    // workgroup w at position w).
+    int32_t g1;
+    int32_t g1_share;
 #ifdef VCPP_GATHER_DUMP
     int32_t* gather_dump;    // checker builds: [rows][gather_stride][2] (block, slot)
     int64_t gather_stride;

@@ -314,15 +314,43 @@ __device__ __forceinline__ int64_t frag_block(int w0, int i, int pairs, int pair
 // Workgroup spans of the split axis (Tv tiles, G ranges walked by WG
 // workgroups, WG <= G): workgroup w covers ranges [range_start(w, G, WG),
 // range_start(w + 1, G, WG)).  With WG == G a span is one range.
-struct Spans {
-    int Tv, G, WG;
-    __device__ int start(int w) const { return range_start(range_start(w, G, WG), Tv, G); }
-    __device__ int span_of(int t) const {
-        const int r = range_of(t, Tv, G);
-        return WG == G ? r : range_of(r, G, WG);
+// The ranges of the split axis (Tv units, G ranges): equal ones
+// [floor(r Tv / G), floor((r + 1) Tv / G)), or, with g1 > 0 (G even),
+// alternating sizes: positions 2k take share / 256 of each pair's units and
+// positions 2k + 1 the rest, so position r starts at
+// Tv cum(r) / (128 G) with cum(r) = 256 (r / 2) + share (r % 2).
+struct Split {
+    int Tv, G, share;
+    __device__ Split(int tv, int g, int g1, int sh) : Tv(tv), G(g), share(g1 > 0 && g % 2 == 0 ? sh : 0) {}
+    __device__ int rstart(int r) const {
+        if (share == 0) return range_start(r, Tv, G);
+        const int64_t cum = (int64_t)(r >> 1) * 256 + (r & 1) * share;
+        return (int)((int64_t)Tv * cum / ((int64_t)G * 128));
     }
-    // Every span holds a tile when every range does (Tv >= G, WG <= G).
-    __device__ bool live(int w) const { return Tv >= G || start(w) < start(w + 1); }
+    __device__ int rof(int t) const {  // the largest r with rstart(r) <= t (0 <= t < Tv)
+        if (share == 0) return range_of(t, Tv, G);
+        const int64_t u = ((int64_t)t * G * 128) / Tv;  // weight units before t, rounded down
+        int r = (int)(u >> 8) * 2 + ((u & 255) >= share ? 1 : 0);
+        while (r + 1 < G && rstart(r + 1) <= t) ++r;
+        while (r > 0 && rstart(r) > t) --r;
+        return r;
+    }
+    // every range holds at least one unit
+    __device__ bool all_live() const {
+        return share == 0 ? Tv >= G : (int64_t)Tv * min(share, 256 - share) >= (int64_t)G * 128;
+    }
+};
+
+struct Spans {
+    Split sp;
+    int WG;  // workgroups walking the G ranges (G: a span is one range)
+    __device__ int start(int w) const { return sp.rstart(WG == sp.G ? w : range_start(w, sp.G, WG)); }
+    __device__ int span_of(int t) const {
+        const int r = sp.rof(t);
+        return WG == sp.G ? r : range_of(r, sp.G, WG);
+    }
+    // Every span holds a tile when every range does (WG <= G).
+    __device__ bool live(int w) const { return sp.all_live() || start(w) < start(w + 1); }
 };
 
 template <int D>
@@ -694,7 +722,7 @@ __global__ __launch_bounds__(256) void merge_split_kernel(DecodeParams p) {
     if (E <= S) return;  // no tiles: zeroed by the decode kernel
     // the split's axis: tile t of s sits at t + X (non-empty sequences up to s)
     const int Tv = T + X * K, shift = X * (KS + 1);
-    const Spans sp{Tv, G, p.page_grid};
+    const Spans sp{Split(Tv, G, p.g1, p.g1_share), p.page_grid};
     const int w0 = sp.span_of(S + shift), w1 = sp.span_of(E - 1 + shift);
     if (w0 == w1) return;  // finished in place
     const int kvh = pair / p.qchunks, qc = pair - kvh * p.qchunks;
@@ -1032,7 +1060,11 @@ __device__ __forceinline__ void decode_page_body(const DecodeParams& p, int bx, 
     // way a workgroup leaves at most one fragment per sequence end, indexed
     // by the workgroup (span_of in the merge kernel).
     const int G = p.num_wg, WG = nbx;
-    const int r_lo = range_start(bx, G, WG), r_hi = range_start(bx + 1, G, WG);
+    // With alternating range sizes the first dispatch round (ids below WG / 2)
+    // takes the even positions of the axis, the second the odd ones; partial
+    // blocks are indexed by position.
+    const int posn = !F && p.g1 > 0 ? (bx < WG / 2 ? 2 * bx : 2 * (bx - WG / 2) + 1) : bx;
+    const int r_lo = range_start(posn, G, WG), r_hi = range_start(posn + 1, G, WG);
     // This workgroup's kv heads: hb .. hb + HW - 1, one per wave (global
     // head kvh; local slot `wave` in the LDS tile).  group <= 8: one query
     // chunk per kv head.
@@ -1108,7 +1140,8 @@ __device__ __forceinline__ void decode_page_body(const DecodeParams& p, int bx, 
         }
         return T;
     };
-    const int a = real_of(range_start(r_lo, Tv, G)), b = real_of(range_start(r_hi, Tv, G));
+    const Split spl(Tv, G, F ? 0 : p.g1, p.g1_share);
+    const int a = real_of(spl.rstart(r_lo)), b = real_of(spl.rstart(r_hi));
     const bool zero_owner_tail = (T == 0 && bx == 0) || (T > 0 && bx == WG - 1);
 
     // Zero the outputs of empty sequences this range owns (wave 0).
@@ -1215,7 +1248,7 @@ __device__ __forceinline__ void decode_page_body(const DecodeParams& p, int bx, 
         const bool odd = (c & 1) != 0;
         const int rr = odd ? rk1 : rk0;
         const int h = 4 * (g & 1) + rr;
-        const int64_t blk = ((int64_t)bx * 2 + slot) * p.pairs + pair;
+        const int64_t blk = ((int64_t)posn * 2 + slot) * p.pairs + pair;
         float* orow = complete ? p.out + ((int64_t)cur * p.num_heads + head_base + h) * D
                                : p.ws_o + (blk * 8 + h) * D;
         float lsel = lh[0];
