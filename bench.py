@@ -654,7 +654,7 @@ def bench_dense(torch, pyvcpp, args):
                        "bytes_per_step": nbytes},
             "roofline": {"bound": "hbm", "achieved": round(tbs * 1e3, 1), "peak": HBM_PEAK_TBS * 1e3,
                          "unit": "GB/s", "frac": round(tbs / HBM_PEAK_TBS, 4),
-                         "kernel": "dense_attention_kernel"}}
+                         "kernel": "dense_attention_dma_kernel"}}
 
 
 def bench_qkprep(torch, pyvcpp, args):

@@ -27,8 +27,14 @@ def run_gpu(q, k, v, mask=None):
     return out.cpu().numpy(), w.cpu().numpy()
 
 
+# Shapes cover both kernel families: the LDS-DMA one-pass kernel (no mask,
+# kv_len <= 4096, head_dim 64/80/96/128: fewer chunks than waves, ragged last
+# chunks, exactly 4096 keys) and the register-load kernels past 4096 keys or at
+# other head dims.
 @pytest.mark.parametrize("shape", [(1, 1, 1, 1, 80), (2, 8, 3, 300, 80), (3, 4, 1, 1000, 128),
-                                   (1, 2, 2, 17, 64), (1, 1, 1, 5000, 96)])
+                                   (1, 2, 2, 17, 64), (1, 1, 1, 5000, 96), (1, 1, 1, 48, 64),
+                                   (1, 4, 1, 33, 128), (2, 3, 1, 4096, 96), (1, 2, 1, 4096, 80),
+                                   (1, 2, 1, 4097, 80), (2, 2, 1, 777, 48)])
 def test_flash_matches_oracle(cuda, shape):
     B, H, ql, kv, D = shape
     q = O.normal(1000 + kv, (B, H, ql, D))

@@ -10,6 +10,8 @@
 // fp32 throughout; this is not a hot path.
 #include "dense.h"
 
+#include <cstdlib>
+
 namespace vcpp {
 
 namespace {
@@ -165,12 +167,217 @@ __global__ __launch_bounds__(kThreads) void dense_attention_vec_kernel(DensePara
     }
 }
 
+// The same (no mask, kv_len <= 4096, D in {64, 80, 96, 128}, 16-byte aligned
+// q/k/v) as one pass over K and V through LDS.  Each wave owns the 16-key
+// chunks wave, wave + 4, ... of the pair; a chunk's K rows and V rows are each
+// one contiguous run, moved into the wave's own LDS ring with
+// global_load_lds_dwordx4 (1 KiB of whole cache lines per instruction,
+// non-temporal: every byte is read once) and waited for on the wave's own
+// vmcnt, so no loop iteration has a compiler-visible global load.  Lane
+// (key lane / 4, quarter lane % 4) dots its quarter of the key row, the quad
+// sums it, and the lane keeps an online softmax over its keys (running max,
+// sum of exp, and the exp-weighted sum of its quarter of the V rows).  The
+// logits stay in LDS; at the end the lanes and waves combine by log-sum-exp
+// and the probabilities exp(l - max) / (sum + 1e-9) are written once.
+template <int D>
+struct DenseDma {
+    static constexpr int ROWB = D * 4;               // bytes of one key row
+    static constexpr int CH = 16 * ROWB;             // one chunk of K (or of V)
+    static constexpr int NI = CH / 1024;             // DMA instructions per chunk of K
+    static constexpr int MAXS = 4096;                // logits held in LDS
+    static constexpr int RED = 4 * (D + 2) * 4;      // per-wave partials
+    static constexpr int STAGES = 4 * 3 * 2 * CH + MAXS * 4 + RED <= 160 * 1024 ? 3 : 2;
+    static constexpr int STAGE = 2 * CH;
+    static constexpr int WAVE = STAGES * STAGE;
+    static constexpr int OFF_LOGIT = 4 * WAVE;
+    static constexpr int OFF_RED = OFF_LOGIT + MAXS * 4;
+    static constexpr int LDS = OFF_RED + RED;
+    static_assert(CH % 1024 == 0 && D % 16 == 0, "chunk shape");
+    static_assert(LDS <= 160 * 1024, "LDS budget");
+    static_assert((STAGES - 1) * 2 * NI < 64, "vmcnt range");
+};
+
+__device__ __attribute__((aligned(16))) const uint32_t kDenseZero16[4] = {0, 0, 0, 0};
+
+__device__ __forceinline__ void dense_dma16(const void* src, uint32_t lds_base) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off nt\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved) : "s"(lds_base), "v"(src) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void dense_wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void dense_attention_dma_kernel(DenseParams p) {
+    using C = DenseDma<D>;
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    constexpr int EQ = D / 4, NQ = EQ / 4;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const int64_t bh = blockIdx.x;
+    const int S = p.kv_len;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int qq = lane & 3, r = lane >> 2;
+    const char* kb = reinterpret_cast<const char*>(p.k + bh * D * S);
+    const char* vb = reinterpret_cast<const char*>(p.v + bh * D * S);
+    const int64_t bytes = (int64_t)S * C::ROWB;
+    const uint32_t wbase = (uint32_t)(uintptr_t)smem + wave * C::WAVE;
+    const int nch = (S + 15) >> 4;
+    const int nloc = nch > wave ? (nch - wave + 3) >> 2 : 0;  // chunks wave, wave + 4, ...
+    float* logit = reinterpret_cast<float*>(smem + C::OFF_LOGIT);
+
+    const float* q = p.q + bh * D * p.q_len;
+    f4 qv[NQ];
+#pragma unroll
+    for (int m = 0; m < NQ; ++m) qv[m] = *reinterpret_cast<const f4*>(q + qq * EQ + 4 * m);
+    // q must be in registers before the first DMA: a wait for it left to its
+    // first use would be a vmcnt wait inside the loop, counted without the
+    // DMAs, and would drain the ring.
+#pragma unroll
+    for (int m = 0; m < NQ; ++m) asm volatile("" : "+v"(qv[m]));
+
+    // Local chunk i into ring stage i % STAGES; past the wave's last chunk
+    // (or past the pair's last key) the lanes read a zero chunk, so every
+    // issue is 2 NI instructions and the waits below have fixed counts.
+    auto issue = [&](int i) {
+        const int64_t off0 = (int64_t)(wave + 4 * i) * C::CH + lane * 16;
+        const uint32_t sb = __builtin_amdgcn_readfirstlane(wbase + (i % C::STAGES) * C::STAGE);
+#pragma unroll
+        for (int j = 0; j < C::NI; ++j) {
+            const int64_t off = off0 + j * 1024;
+            const bool ok = i < nloc && off < bytes;
+            dense_dma16(ok ? (const void*)(kb + off) : (const void*)kDenseZero16, sb + j * 1024);
+        }
+#pragma unroll
+        for (int j = 0; j < C::NI; ++j) {
+            const int64_t off = off0 + j * 1024;
+            const bool ok = i < nloc && off < bytes;
+            dense_dma16(ok ? (const void*)(vb + off) : (const void*)kDenseZero16, sb + C::CH + j * 1024);
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < C::STAGES - 1; ++i) issue(i);
+
+    const float scale = 1.0f / sqrtf((float)D);
+    float mx = -__builtin_inff(), sum = 0.0f;
+    f4 acc[NQ];
+#pragma unroll
+    for (int m = 0; m < NQ; ++m) acc[m] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < nloc; ++i) {
+        // the stage about to be refilled was read in the previous iteration
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        issue(i + C::STAGES - 1);
+        dense_wait_vm<(C::STAGES - 1) * 2 * C::NI>();
+        const char* st = smem + wave * C::WAVE + (i % C::STAGES) * C::STAGE + r * C::ROWB + qq * EQ * 4;
+        float dot = 0.0f;
+#pragma unroll
+        for (int m = 0; m < NQ; ++m) {
+            const f4 x = *reinterpret_cast<const f4*>(st + 16 * m);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dot += qv[m][e] * x[e];
+        }
+        dot += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, dot), 0xB1, 0xF, 0xF, false));
+        dot += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, dot), 0x4E, 0xF, 0xF, false));
+        const int s = (wave + 4 * i) * 16 + r;
+        const float l = dot * scale;
+        if (s < S) {
+            if (qq == 0) logit[s] = l;
+            if (l > mx) {
+                const float f = expf(mx - l);
+                sum *= f;
+#pragma unroll
+                for (int m = 0; m < NQ; ++m) acc[m] *= f;
+                mx = l;
+            }
+            const float e = expf(l - mx);
+            sum += e;
+#pragma unroll
+            for (int m = 0; m < NQ; ++m) acc[m] += e * *reinterpret_cast<const f4*>(st + C::CH + 16 * m);
+        }
+    }
+    dense_wait_vm<0>();
+
+    // Lanes -> wave: max over the wave, rescale, sum over the 16 key lanes of
+    // each quarter.
+    float wm = mx;
+    for (int o = 1; o < 64; o <<= 1) wm = fmaxf(wm, __shfl_xor(wm, o, 64));
+    const float f = mx == -__builtin_inff() ? 0.0f : expf(mx - wm);
+    sum *= f;
+#pragma unroll
+    for (int m = 0; m < NQ; ++m) acc[m] *= f;
+    for (int o = 4; o < 64; o <<= 1) {
+        sum += __shfl_xor(sum, o, 64);
+#pragma unroll
+        for (int m = 0; m < NQ; ++m)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[m][e] += __shfl_xor(acc[m][e], o, 64);
+    }
+    float* red = reinterpret_cast<float*>(smem + C::OFF_RED);  // [4][D] sums, [4] max, [4] sum
+    if (r == 0) {
+#pragma unroll
+        for (int m = 0; m < NQ; ++m) *reinterpret_cast<f4*>(red + wave * D + qq * EQ + 4 * m) = acc[m];
+    }
+    if (lane == 0) {
+        red[4 * D + wave] = wm;
+        red[4 * D + 4 + wave] = sum;
+    }
+    __syncthreads();  // logits and the per-wave partials of every wave
+
+    // Waves -> pair.
+    float gm = red[4 * D];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) gm = fmaxf(gm, red[4 * D + w]);
+    float fw[4], total = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const float mw = red[4 * D + w];
+        fw[w] = mw == -__builtin_inff() ? 0.0f : expf(mw - gm);
+        total += red[4 * D + 4 + w] * fw[w];
+    }
+    const float inv = 1.0f / (total + 1e-9f);
+    for (int d = threadIdx.x; d < D; d += kThreads) {
+        float o = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) o += red[w * D + d] * fw[w];
+        p.out[bh * D + d] = o * inv;
+    }
+    float* wout = p.attn_weights + bh * S;
+    for (int s = threadIdx.x; s < S; s += kThreads) wout[s] = expf(logit[s] - gm) * inv;
+}
+
+template <int D>
+hipError_t launch_dense_dma(const DenseParams& p, hipStream_t stream) {
+    using C = DenseDma<D>;
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(dense_attention_dma_kernel<D>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL(dense_attention_dma_kernel<D>, dim3(p.batch * p.heads), dim3(kThreads), C::LDS, stream, p);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+// VCPP_DENSE_DMA=0 keeps the register-load kernels (for measurement).
+static bool dense_dma_off() {
+    static const bool off = [] {
+        const char* e = std::getenv("VCPP_DENSE_DMA");
+        return e && e[0] == '0';
+    }();
+    return off;
+}
 
 hipError_t launch_dense(const DenseParams& p, hipStream_t stream) {
     const dim3 grid(p.batch * p.heads), block(kThreads);
     auto al = [](const void* x) { return reinterpret_cast<uintptr_t>(x) % 16 == 0; };
     const bool vec = al(p.q) && al(p.k) && al(p.v) && p.kv_len > 0;
+    const bool dma = vec && !p.mask && p.kv_len <= 4096 && !dense_dma_off();
+    if (dma && p.head_dim == 64) return launch_dense_dma<64>(p, stream);
+    if (dma && p.head_dim == 80) return launch_dense_dma<80>(p, stream);
+    if (dma && p.head_dim == 96) return launch_dense_dma<96>(p, stream);
+    if (dma && p.head_dim == 128) return launch_dense_dma<128>(p, stream);
     if (vec && p.head_dim == 64) hipLaunchKernelGGL(dense_attention_vec_kernel<64>, grid, block, 0, stream, p);
     else if (vec && p.head_dim == 80) hipLaunchKernelGGL(dense_attention_vec_kernel<80>, grid, block, 0, stream, p);
     else if (vec && p.head_dim == 128) hipLaunchKernelGGL(dense_attention_vec_kernel<128>, grid, block, 0, stream, p);
