@@ -12,6 +12,10 @@
 
 #include <cstdlib>
 
+#ifndef VCPP_DENSE_NW
+#define VCPP_DENSE_NW 4
+#endif
+
 namespace vcpp {
 
 namespace {
@@ -179,17 +183,17 @@ __global__ __launch_bounds__(kThreads) void dense_attention_vec_kernel(DensePara
 // sum of exp, and the exp-weighted sum of its quarter of the V rows).  The
 // logits stay in LDS; at the end the lanes and waves combine by log-sum-exp
 // and the probabilities exp(l - max) / (sum + 1e-9) are written once.
-template <int D>
+template <int D, int NW>
 struct DenseDma {
     static constexpr int ROWB = D * 4;               // bytes of one key row
     static constexpr int CH = 16 * ROWB;             // one chunk of K (or of V)
     static constexpr int NI = CH / 1024;             // DMA instructions per chunk of K
     static constexpr int MAXS = 4096;                // logits held in LDS
-    static constexpr int RED = 4 * (D + 2) * 4;      // per-wave partials
-    static constexpr int STAGES = 4 * 3 * 2 * CH + MAXS * 4 + RED <= 160 * 1024 ? 3 : 2;
+    static constexpr int RED = NW * (D + 2) * 4;     // per-wave partials
+    static constexpr int STAGES = NW * 3 * 2 * CH + MAXS * 4 + RED <= 160 * 1024 ? 3 : 2;
     static constexpr int STAGE = 2 * CH;
     static constexpr int WAVE = STAGES * STAGE;
-    static constexpr int OFF_LOGIT = 4 * WAVE;
+    static constexpr int OFF_LOGIT = NW * WAVE;
     static constexpr int OFF_RED = OFF_LOGIT + MAXS * 4;
     static constexpr int LDS = OFF_RED + RED;
     static_assert(CH % 1024 == 0 && D % 16 == 0, "chunk shape");
@@ -210,9 +214,9 @@ __device__ __forceinline__ void dense_wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int D>
-__global__ __launch_bounds__(kThreads) void dense_attention_dma_kernel(DenseParams p) {
-    using C = DenseDma<D>;
+template <int D, int NW>
+__global__ __launch_bounds__(NW * 64) void dense_attention_dma_kernel(DenseParams p) {
+    using C = DenseDma<D, NW>;
     typedef float f4 __attribute__((ext_vector_type(4)));
     constexpr int EQ = D / 4, NQ = EQ / 4;
     extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -225,7 +229,7 @@ __global__ __launch_bounds__(kThreads) void dense_attention_dma_kernel(DensePara
     const int64_t bytes = (int64_t)S * C::ROWB;
     const uint32_t wbase = (uint32_t)(uintptr_t)smem + wave * C::WAVE;
     const int nch = (S + 15) >> 4;
-    const int nloc = nch > wave ? (nch - wave + 3) >> 2 : 0;  // chunks wave, wave + 4, ...
+    const int nloc = nch > wave ? (nch - wave + NW - 1) / NW : 0;  // chunks wave, wave + NW, ...
     float* logit = reinterpret_cast<float*>(smem + C::OFF_LOGIT);
 
     const float* q = p.q + bh * D * p.q_len;
@@ -242,7 +246,7 @@ __global__ __launch_bounds__(kThreads) void dense_attention_dma_kernel(DensePara
     // (or past the pair's last key) the lanes read a zero chunk, so every
     // issue is 2 NI instructions and the waits below have fixed counts.
     auto issue = [&](int i) {
-        const int64_t off0 = (int64_t)(wave + 4 * i) * C::CH + lane * 16;
+        const int64_t off0 = (int64_t)(wave + NW * i) * C::CH + lane * 16;
         const uint32_t sb = __builtin_amdgcn_readfirstlane(wbase + (i % C::STAGES) * C::STAGE);
 #pragma unroll
         for (int j = 0; j < C::NI; ++j) {
@@ -280,7 +284,7 @@ __global__ __launch_bounds__(kThreads) void dense_attention_dma_kernel(DensePara
         }
         dot += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, dot), 0xB1, 0xF, 0xF, false));
         dot += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, dot), 0x4E, 0xF, 0xF, false));
-        const int s = (wave + 4 * i) * 16 + r;
+        const int s = (wave + NW * i) * 16 + r;
         const float l = dot * scale;
         if (s < S) {
             if (qq == 0) logit[s] = l;
@@ -314,47 +318,48 @@ __global__ __launch_bounds__(kThreads) void dense_attention_dma_kernel(DensePara
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[m][e] += __shfl_xor(acc[m][e], o, 64);
     }
-    float* red = reinterpret_cast<float*>(smem + C::OFF_RED);  // [4][D] sums, [4] max, [4] sum
+    float* red = reinterpret_cast<float*>(smem + C::OFF_RED);  // [NW][D] sums, [NW] max, [NW] sum
     if (r == 0) {
 #pragma unroll
         for (int m = 0; m < NQ; ++m) *reinterpret_cast<f4*>(red + wave * D + qq * EQ + 4 * m) = acc[m];
     }
     if (lane == 0) {
-        red[4 * D + wave] = wm;
-        red[4 * D + 4 + wave] = sum;
+        red[NW * D + wave] = wm;
+        red[NW * D + NW + wave] = sum;
     }
     __syncthreads();  // logits and the per-wave partials of every wave
 
     // Waves -> pair.
-    float gm = red[4 * D];
+    float gm = red[NW * D];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) gm = fmaxf(gm, red[4 * D + w]);
-    float fw[4], total = 0.0f;
+    for (int w = 1; w < NW; ++w) gm = fmaxf(gm, red[NW * D + w]);
+    float fw[NW], total = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        const float mw = red[4 * D + w];
+    for (int w = 0; w < NW; ++w) {
+        const float mw = red[NW * D + w];
         fw[w] = mw == -__builtin_inff() ? 0.0f : expf(mw - gm);
-        total += red[4 * D + 4 + w] * fw[w];
+        total += red[NW * D + NW + w] * fw[w];
     }
     const float inv = 1.0f / (total + 1e-9f);
-    for (int d = threadIdx.x; d < D; d += kThreads) {
+    for (int d = threadIdx.x; d < D; d += NW * 64) {
         float o = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) o += red[w * D + d] * fw[w];
+        for (int w = 0; w < NW; ++w) o += red[w * D + d] * fw[w];
         p.out[bh * D + d] = o * inv;
     }
     float* wout = p.attn_weights + bh * S;
-    for (int s = threadIdx.x; s < S; s += kThreads) wout[s] = expf(logit[s] - gm) * inv;
+    for (int s = threadIdx.x; s < S; s += NW * 64) wout[s] = expf(logit[s] - gm) * inv;
 }
 
 template <int D>
 hipError_t launch_dense_dma(const DenseParams& p, hipStream_t stream) {
-    using C = DenseDma<D>;
+    constexpr int NW = VCPP_DENSE_NW;
+    using C = DenseDma<D, NW>;
     static const hipError_t attr =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(dense_attention_dma_kernel<D>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(dense_attention_dma_kernel<D, NW>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL(dense_attention_dma_kernel<D>, dim3(p.batch * p.heads), dim3(kThreads), C::LDS, stream, p);
+    hipLaunchKernelGGL((dense_attention_dma_kernel<D, NW>), dim3(p.batch * p.heads), dim3(NW * 64), C::LDS, stream, p);
     return hipGetLastError();
 }
 
