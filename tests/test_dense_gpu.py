@@ -27,14 +27,14 @@ def run_gpu(q, k, v, mask=None):
     return out.cpu().numpy(), w.cpu().numpy()
 
 
-# Shapes cover both kernel families: the LDS-DMA one-pass kernel (no mask,
-# kv_len <= 4096, head_dim 64/80/96/128: fewer chunks than waves, ragged last
-# chunks, exactly 4096 keys) and the register-load kernels past 4096 keys or at
-# other head dims.
+# Shapes cover the LDS-DMA one-pass kernel (head_dim 64/80/96/128: fewer
+# chunks than waves, ragged last chunks, exactly one 4096-key logit segment,
+# one key past it, three segments) and the plain kernel at another head dim.
 @pytest.mark.parametrize("shape", [(1, 1, 1, 1, 80), (2, 8, 3, 300, 80), (3, 4, 1, 1000, 128),
                                    (1, 2, 2, 17, 64), (1, 1, 1, 5000, 96), (1, 1, 1, 48, 64),
                                    (1, 4, 1, 33, 128), (2, 3, 1, 4096, 96), (1, 2, 1, 4096, 80),
-                                   (1, 2, 1, 4097, 80), (2, 2, 1, 777, 48)])
+                                   (1, 2, 1, 4097, 80), (1, 2, 1, 9001, 64), (1, 1, 1, 12288, 128),
+                                   (2, 2, 1, 777, 48)])
 def test_flash_matches_oracle(cuda, shape):
     B, H, ql, kv, D = shape
     q = O.normal(1000 + kv, (B, H, ql, D))
@@ -57,3 +57,33 @@ def test_flash_mask(cuda):
     assert_close(got, want, 1e-4, 1e-4, what="flash masked out")
     assert_close(got_w, want_w, 1e-5, 1e-4, what="flash masked weights")
     assert np.all(got_w[:, mask < 0] == 0.0)
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 1, 33, 64), (2, 3, 1, 200, 80), (1, 2, 1, 4100, 96),
+                                   (1, 1, 1, 8200, 128), (1, 1, 1, 100, 48)])
+def test_flash_mask_shapes(cuda, shape):
+    """Masks through the one-pass kernel's DMA ring (and the plain kernel at
+    head_dim 48): masked keys get probability 0 and leave the output."""
+    B, H, ql, kv, D = shape
+    q = O.normal(21 + kv, (B, H, ql, D))
+    k = O.normal(22 + kv, (B, H, kv, D))
+    v = O.normal(23 + kv, (B, H, kv, D))
+    mask = np.where(O.normal(24 + kv, (kv,)) > 0.0, 0.0, -1.0).astype(np.float32)
+    want, want_w = O.flash(q, k, v, mask)
+    got, got_w = run_gpu(q, k, v, mask)
+    assert_close(got, want, 1e-4, 1e-4, what="flash masked out %s" % (shape,))
+    assert_close(got_w, want_w, 1e-5, 1e-4, what="flash masked weights %s" % (shape,))
+    assert np.all(got_w[:, mask < 0] == 0.0)
+
+
+def test_flash_all_masked(cuda):
+    """Every key masked: the reference's -1e9 logits give uniform weights."""
+    B, H, ql, kv, D = 1, 2, 1, 50, 80
+    q = O.normal(31, (B, H, ql, D))
+    k = O.normal(32, (B, H, kv, D))
+    v = O.normal(33, (B, H, kv, D))
+    mask = np.full((kv,), -1.0, dtype=np.float32)
+    want, want_w = O.flash(q, k, v, mask)
+    got, got_w = run_gpu(q, k, v, mask)
+    assert_close(got, want, 1e-4, 1e-4, what="flash all masked out")
+    assert_close(got_w, want_w, 1e-5, 1e-4, what="flash all masked weights")

@@ -171,34 +171,39 @@ __global__ __launch_bounds__(kThreads) void dense_attention_vec_kernel(DensePara
     }
 }
 
-// The same (no mask, kv_len <= 4096, D in {64, 80, 96, 128}, 16-byte aligned
-// q/k/v) as one pass over K and V through LDS.  Each wave owns the 16-key
-// chunks wave, wave + 4, ... of the pair; a chunk's K rows and V rows are each
-// one contiguous run, moved into the wave's own LDS ring with
+// The same (head_dim 64, 80, 96 or 128, 16-byte aligned q/k/v) as one pass
+// over K and V through LDS.  Each wave owns the 16-key chunks wave,
+// wave + NW, ... of the pair; a chunk's K rows and V rows are each one
+// contiguous run, moved into the wave's own LDS ring with
 // global_load_lds_dwordx4 (1 KiB of whole cache lines per instruction,
-// non-temporal: every byte is read once) and waited for on the wave's own
-// vmcnt, so no loop iteration has a compiler-visible global load.  Lane
-// (key lane / 4, quarter lane % 4) dots its quarter of the key row, the quad
-// sums it, and the lane keeps an online softmax over its keys (running max,
-// sum of exp, and the exp-weighted sum of its quarter of the V rows).  The
-// logits stay in LDS; at the end the lanes and waves combine by log-sum-exp
-// and the probabilities exp(l - max) / (sum + 1e-9) are written once.
-template <int D, int NW>
+// non-temporal: every byte is read once), with the chunk's 16 mask values
+// when there is a mask, and waited for on the wave's own vmcnt, so no loop
+// iteration has a compiler-visible global load.  Lane (key lane / 4, quarter
+// lane % 4) dots its quarter of the key row, the quad sums it, and the lane
+// keeps an online softmax over its keys (running max, sum of exp, and the
+// exp-weighted sum of its quarter of the V rows).  The logits stay in LDS, in
+// segments of 4096 keys; a full segment is flushed to attn_weights before
+// the next one reuses the space.  At the end the lanes and waves combine by
+// log-sum-exp and the probabilities exp(l - max) / (sum + 1e-9) are written.
+template <int D, int NW, bool MASK>
 struct DenseDma {
     static constexpr int ROWB = D * 4;               // bytes of one key row
     static constexpr int CH = 16 * ROWB;             // one chunk of K (or of V)
     static constexpr int NI = CH / 1024;             // DMA instructions per chunk of K
-    static constexpr int MAXS = 4096;                // logits held in LDS
+    static constexpr int NM = MASK ? 1 : 0;          // mask instruction per chunk
+    static constexpr int NPER = 2 * NI + NM;         // DMA instructions per chunk
+    static constexpr int MAXS = 4096;                // logits held in LDS (one segment)
+    static constexpr int SEGI = MAXS / 16 / NW;      // local chunks per segment
     static constexpr int RED = NW * (D + 2) * 4;     // per-wave partials
-    static constexpr int STAGES = NW * 3 * 2 * CH + MAXS * 4 + RED <= 160 * 1024 ? 3 : 2;
-    static constexpr int STAGE = 2 * CH;
+    static constexpr int STAGE = 2 * CH + (MASK ? 256 : 0);  // K, V, the mask dwords
+    static constexpr int STAGES = NW * 3 * STAGE + MAXS * 4 + RED <= 160 * 1024 ? 3 : 2;
     static constexpr int WAVE = STAGES * STAGE;
     static constexpr int OFF_LOGIT = NW * WAVE;
     static constexpr int OFF_RED = OFF_LOGIT + MAXS * 4;
     static constexpr int LDS = OFF_RED + RED;
     static_assert(CH % 1024 == 0 && D % 16 == 0, "chunk shape");
     static_assert(LDS <= 160 * 1024, "LDS budget");
-    static_assert((STAGES - 1) * 2 * NI < 64, "vmcnt range");
+    static_assert((STAGES - 1) * NPER < 64, "vmcnt range");
 };
 
 __device__ __attribute__((aligned(16))) const uint32_t kDenseZero16[4] = {0, 0, 0, 0};
@@ -209,14 +214,21 @@ __device__ __forceinline__ void dense_dma16(const void* src, uint32_t lds_base) 
                  : "=&s"(saved) : "s"(lds_base), "v"(src) : "memory");
 }
 
+// 4 bytes per lane (lane l lands at lds_base + 4 l).
+__device__ __forceinline__ void dense_dma4(const void* src, uint32_t lds_base) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dword %2, off nt\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved) : "s"(lds_base), "v"(src) : "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void dense_wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int D, int NW>
+template <int D, int NW, bool MASK>
 __global__ __launch_bounds__(NW * 64) void dense_attention_dma_kernel(DenseParams p) {
-    using C = DenseDma<D, NW>;
+    using C = DenseDma<D, NW, MASK>;
     typedef float f4 __attribute__((ext_vector_type(4)));
     constexpr int EQ = D / 4, NQ = EQ / 4;
     extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -229,8 +241,12 @@ __global__ __launch_bounds__(NW * 64) void dense_attention_dma_kernel(DenseParam
     const int64_t bytes = (int64_t)S * C::ROWB;
     const uint32_t wbase = (uint32_t)(uintptr_t)smem + wave * C::WAVE;
     const int nch = (S + 15) >> 4;
-    const int nloc = nch > wave ? (nch - wave + NW - 1) / NW : 0;  // chunks wave, wave + NW, ...
+    // Every wave runs the same number of iterations (chunks past the last
+    // one are zero loads and no keys), so that all of them reach each
+    // segment flush.
+    const int nit = (nch + NW - 1) / NW;
     float* logit = reinterpret_cast<float*>(smem + C::OFF_LOGIT);
+    float* wout = p.attn_weights + bh * S;
 
     const float* q = p.q + bh * D * p.q_len;
     f4 qv[NQ];
@@ -242,23 +258,26 @@ __global__ __launch_bounds__(NW * 64) void dense_attention_dma_kernel(DenseParam
 #pragma unroll
     for (int m = 0; m < NQ; ++m) asm volatile("" : "+v"(qv[m]));
 
-    // Local chunk i into ring stage i % STAGES; past the wave's last chunk
-    // (or past the pair's last key) the lanes read a zero chunk, so every
-    // issue is 2 NI instructions and the waits below have fixed counts.
+    // Local chunk i into ring stage i % STAGES; lanes past the pair's last
+    // key read a zero chunk, so every issue is NPER instructions and the
+    // waits below have fixed counts.
     auto issue = [&](int i) {
-        const int64_t off0 = (int64_t)(wave + NW * i) * C::CH + lane * 16;
+        const int c = wave + NW * i;
+        const int64_t off0 = (int64_t)c * C::CH + lane * 16;
         const uint32_t sb = __builtin_amdgcn_readfirstlane(wbase + (i % C::STAGES) * C::STAGE);
 #pragma unroll
         for (int j = 0; j < C::NI; ++j) {
             const int64_t off = off0 + j * 1024;
-            const bool ok = i < nloc && off < bytes;
-            dense_dma16(ok ? (const void*)(kb + off) : (const void*)kDenseZero16, sb + j * 1024);
+            dense_dma16(off < bytes ? (const void*)(kb + off) : (const void*)kDenseZero16, sb + j * 1024);
         }
 #pragma unroll
         for (int j = 0; j < C::NI; ++j) {
             const int64_t off = off0 + j * 1024;
-            const bool ok = i < nloc && off < bytes;
-            dense_dma16(ok ? (const void*)(vb + off) : (const void*)kDenseZero16, sb + C::CH + j * 1024);
+            dense_dma16(off < bytes ? (const void*)(vb + off) : (const void*)kDenseZero16, sb + C::CH + j * 1024);
+        }
+        if constexpr (MASK) {  // lanes 0-15: the chunk's mask values
+            const int s = 16 * c + lane;
+            dense_dma4(lane < 16 && s < S ? (const void*)(p.mask + s) : (const void*)kDenseZero16, sb + 2 * C::CH);
         }
     };
 #pragma unroll
@@ -269,12 +288,23 @@ __global__ __launch_bounds__(NW * 64) void dense_attention_dma_kernel(DenseParam
     f4 acc[NQ];
 #pragma unroll
     for (int m = 0; m < NQ; ++m) acc[m] = f4{0.f, 0.f, 0.f, 0.f};
-    for (int i = 0; i < nloc; ++i) {
+    for (int i = 0; i < nit; ++i) {
+        if (S > C::MAXS && i > 0 && i % C::SEGI == 0) {
+            // Keys [i / SEGI - 1 segments, ...) are done: flush the segment's
+            // logits.  The ring is drained first (the stores then wait on
+            // nothing of it), and the chunks already issued stay in LDS.
+            dense_wait_vm<0>();
+            __syncthreads();
+            const int seg0 = (i / C::SEGI - 1) * C::MAXS;
+            for (int e = threadIdx.x; e < C::MAXS; e += NW * 64) wout[seg0 + e] = logit[e];
+            __syncthreads();
+        }
         // the stage about to be refilled was read in the previous iteration
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         issue(i + C::STAGES - 1);
-        dense_wait_vm<(C::STAGES - 1) * 2 * C::NI>();
-        const char* st = smem + wave * C::WAVE + (i % C::STAGES) * C::STAGE + r * C::ROWB + qq * EQ * 4;
+        dense_wait_vm<(C::STAGES - 1) * C::NPER>();
+        const char* sbase = smem + wave * C::WAVE + (i % C::STAGES) * C::STAGE;
+        const char* st = sbase + r * C::ROWB + qq * EQ * 4;
         float dot = 0.0f;
 #pragma unroll
         for (int m = 0; m < NQ; ++m) {
@@ -285,9 +315,12 @@ __global__ __launch_bounds__(NW * 64) void dense_attention_dma_kernel(DenseParam
         dot += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, dot), 0xB1, 0xF, 0xF, false));
         dot += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, dot), 0x4E, 0xF, 0xF, false));
         const int s = (wave + NW * i) * 16 + r;
-        const float l = dot * scale;
+        float l = dot * scale;
+        if constexpr (MASK) {
+            if (*reinterpret_cast<const float*>(sbase + 2 * C::CH + r * 4) < 0.0f) l = -1e9f;
+        }
         if (s < S) {
-            if (qq == 0) logit[s] = l;
+            if (qq == 0) logit[s & (C::MAXS - 1)] = l;
             if (l > mx) {
                 const float f = expf(mx - l);
                 sum *= f;
@@ -301,7 +334,7 @@ __global__ __launch_bounds__(NW * 64) void dense_attention_dma_kernel(DenseParam
             for (int m = 0; m < NQ; ++m) acc[m] += e * *reinterpret_cast<const f4*>(st + C::CH + 16 * m);
         }
     }
-    dense_wait_vm<0>();
+    dense_wait_vm<0>();  // the ring's padding loads and the segment flushes
 
     // Lanes -> wave: max over the wave, rescale, sum over the 16 key lanes of
     // each quarter.
@@ -347,20 +380,31 @@ __global__ __launch_bounds__(NW * 64) void dense_attention_dma_kernel(DenseParam
         for (int w = 0; w < NW; ++w) o += red[w * D + d] * fw[w];
         p.out[bh * D + d] = o * inv;
     }
-    float* wout = p.attn_weights + bh * S;
-    for (int s = threadIdx.x; s < S; s += NW * 64) wout[s] = expf(logit[s] - gm) * inv;
+    // Probabilities: the last segment's logits from LDS, earlier ones from
+    // attn_weights (written above by this same thread: the same index map).
+    const int last0 = ((S - 1) / C::MAXS) * C::MAXS;
+    for (int s = threadIdx.x; s < S; s += NW * 64) {
+        const float l = s >= last0 ? logit[s - last0] : wout[s];
+        wout[s] = expf(l - gm) * inv;
+    }
+}
+
+template <int D, bool MASK>
+hipError_t launch_dense_dma(const DenseParams& p, hipStream_t stream) {
+    constexpr int NW = VCPP_DENSE_NW;
+    using C = DenseDma<D, NW, MASK>;
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(dense_attention_dma_kernel<D, NW, MASK>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL((dense_attention_dma_kernel<D, NW, MASK>), dim3(p.batch * p.heads), dim3(NW * 64), C::LDS,
+                       stream, p);
+    return hipGetLastError();
 }
 
 template <int D>
 hipError_t launch_dense_dma(const DenseParams& p, hipStream_t stream) {
-    constexpr int NW = VCPP_DENSE_NW;
-    using C = DenseDma<D, NW>;
-    static const hipError_t attr =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(dense_attention_dma_kernel<D, NW>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
-    if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((dense_attention_dma_kernel<D, NW>), dim3(p.batch * p.heads), dim3(NW * 64), C::LDS, stream, p);
-    return hipGetLastError();
+    return p.mask ? launch_dense_dma<D, true>(p, stream) : launch_dense_dma<D, false>(p, stream);
 }
 
 }  // namespace
@@ -378,7 +422,7 @@ hipError_t launch_dense(const DenseParams& p, hipStream_t stream) {
     const dim3 grid(p.batch * p.heads), block(kThreads);
     auto al = [](const void* x) { return reinterpret_cast<uintptr_t>(x) % 16 == 0; };
     const bool vec = al(p.q) && al(p.k) && al(p.v) && p.kv_len > 0;
-    const bool dma = vec && !p.mask && p.kv_len <= 4096 && !dense_dma_off();
+    const bool dma = vec && !dense_dma_off();
     if (dma && p.head_dim == 64) return launch_dense_dma<64>(p, stream);
     if (dma && p.head_dim == 80) return launch_dense_dma<80>(p, stream);
     if (dma && p.head_dim == 96) return launch_dense_dma<96>(p, stream);
