@@ -69,10 +69,12 @@ constexpr int64_t kMaxRanges = 1 << 20;
 // pages (half the bytes per tile) measured the same at 2, 3 and 4.
 constexpr int kSwitchTiles = 2;
 // Byte pages' alternating ranges: the first dispatch round's share of each
-// pair of neighbouring ranges, / 256.  On BASELINE config 5 (int8) 152-164
-// gave the step 2.6-2.7 % over equal ranges, on FP8 pages 176 the kernel
-// 3.5 %; 164 sits between.
-constexpr int kRoundShare = 164;
+// pair of neighbouring ranges, / 256, per page dtype.  int8 on BASELINE
+// config 5: 164 (step 0.233 ms against 0.238 at 180, 2.6 % over equal
+// ranges); FP8 on config 2's sequences: 180 (kernel 40.7-41.1 us against
+// 41.3 at 164 and 42.1-42.3 with equal ranges).
+constexpr int kRoundShareI8 = 164;
+constexpr int kRoundShareFp8 = 180;
 
 int32_t ceil_div(int64_t a, int64_t b) { return (int32_t)((a + b - 1) / b); }
 
@@ -226,14 +228,14 @@ DecodePlan plan_decode(const vcpp_kv_pages* kv, int32_t num_seqs, int32_t num_he
     // Byte pages at two workgroups per CU: the dispatcher places ids 0 ..
     // CUs - 1 first, and those start their rings while the second round's
     // workgroups still build their tile lists.  Ranges alternate in size
-    // along the split axis, the first round's taking kRoundShare / 256 of
-    // each pair of neighbours (VCPP_DECODE_ROUND_SHARE overrides; 128:
-    // equal ranges).
+    // along the split axis, the first round's taking kRoundShareI8 (int8) or
+    // kRoundShareFp8 (FP8) 256ths of each pair of neighbours
+    // (VCPP_DECODE_ROUND_SHARE overrides; 128: equal ranges).
     if (pl.page_mode && fused_grid == 0 && partition_size == 0 && pl.page_grid == pl.num_wg &&
         vcpp::decode_page_wg_per_cu(kv->dtype, kv->num_kv_heads, D) == 2 && bytes &&
         pl.num_wg == page_ranges && pl.num_wg % 2 == 0) {
         const char* rs = getenv("VCPP_DECODE_ROUND_SHARE");
-        const int share = rs ? atoi(rs) : kRoundShare;
+        const int share = rs ? atoi(rs) : kv->dtype == VCPP_KV_FP8 ? kRoundShareFp8 : kRoundShareI8;
         if (share > 0 && share < 256 && share != 128) {
             pl.g1 = pl.num_wg / 2;
             pl.g1_share = share;
