@@ -393,10 +393,16 @@ template <int D, bool MASK>
 hipError_t launch_dense_dma(const DenseParams& p, hipStream_t stream) {
     constexpr int NW = VCPP_DENSE_NW;
     using C = DenseDma<D, NW, MASK>;
-    static const hipError_t attr =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(dense_attention_dma_kernel<D, NW, MASK>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
-    if (attr != hipSuccess) return attr;
+    // The LDS limit is a per-device property of the kernel: raise it once on
+    // each device the library launches on (idempotent if two threads race).
+    static bool attr_set[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || !attr_set[dev]) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(dense_attention_dma_kernel<D, NW, MASK>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+        if (e != hipSuccess) return e;
+        if (dev >= 0 && dev < 64) attr_set[dev] = true;
+    }
     hipLaunchKernelGGL((dense_attention_dma_kernel<D, NW, MASK>), dim3(p.batch * p.heads), dim3(NW * 64), C::LDS,
                        stream, p);
     return hipGetLastError();
