@@ -87,3 +87,59 @@ def test_flash_all_masked(cuda):
     got, got_w = run_gpu(q, k, v, mask)
     assert_close(got, want, 1e-4, 1e-4, what="flash all masked out")
     assert_close(got_w, want_w, 1e-5, 1e-4, what="flash all masked weights")
+
+
+_CHILD = r"""
+import sys
+import numpy as np
+import torch
+sys.path.insert(0, sys.argv[2])
+import pyvcpp
+a = np.load(sys.argv[1] + "/in.npz")
+outs = {}
+for i in range(int(a["n"])):
+    q, k, v = (torch.from_numpy(a["%s%d" % (x, i)]).to("cuda:0") for x in "qkv")
+    m = a["m%d" % i]
+    md = torch.from_numpy(m).to("cuda:0") if m.size else None
+    B, H, ql, D = q.shape
+    kv = k.shape[2]
+    out = torch.full((B, H, D), float("nan"), device="cuda:0")
+    w = torch.full((B * H, kv), float("nan"), device="cuda:0")
+    pyvcpp.lib().flash_attention_cuda(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), w.data_ptr(),
+                                      B, H, D, ql, kv, None if md is None else md.data_ptr())
+    torch.cuda.synchronize()
+    assert pyvcpp.last_error() == ""
+    outs["o%d" % i] = out.cpu().numpy()
+    outs["w%d" % i] = w.cpu().numpy()
+np.savez(sys.argv[1] + "/out.npz", **outs)
+"""
+
+
+def test_flash_register_kernels(cuda, tmp_path):
+    """The register-load kernels (dense_attention_vec_kernel at head_dim
+    64 / 80 / 128, kept behind VCPP_DENSE_DMA=0, which the library reads once
+    per process): one child process runs a few shapes with the switch set."""
+    import os
+    import subprocess
+    import sys
+    shapes = [(2, 3, 1, 300, 64, False), (1, 4, 2, 1000, 80, True), (1, 2, 1, 5000, 128, False)]
+    arrays, wants = {"n": np.array(len(shapes))}, []
+    for i, (B, H, ql, kv, D, masked) in enumerate(shapes):
+        q = O.normal(41 + i, (B, H, ql, D))
+        k = O.normal(51 + i, (B, H, kv, D))
+        v = O.normal(61 + i, (B, H, kv, D))
+        mask = np.where(O.normal(71 + i, (kv,)) > 0.0, 0.0, -1.0).astype(np.float32) if masked else None
+        arrays.update({"q%d" % i: q.astype(np.float32), "k%d" % i: k.astype(np.float32),
+                       "v%d" % i: v.astype(np.float32),
+                       "m%d" % i: mask if masked else np.zeros((0,), np.float32)})
+        wants.append(O.flash(q, k, v, mask))
+    np.savez(tmp_path / "in.npz", **arrays)
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, VCPP_DENSE_DMA="0")
+    r = subprocess.run([sys.executable, "-c", _CHILD, str(tmp_path), os.path.join(root, "vllm-cpp_amd")],
+                       env=env, capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stderr[-2000:]
+    got = np.load(tmp_path / "out.npz")
+    for i, (want, want_w) in enumerate(wants):
+        assert_close(got["o%d" % i], want, 1e-4, 1e-4, what="flash register kernels out %s" % (shapes[i],))
+        assert_close(got["w%d" % i], want_w, 1e-5, 1e-4, what="flash register kernels weights %s" % (shapes[i],))
